@@ -1,0 +1,165 @@
+/*
+ * kandiga_amd.h -- C ABI of the MI355X routed-expert MoE layer (libkandiga_amd.so).
+ *
+ * Plain pointers and sizes only.  "device" pointers are HIP device memory; `stream` is a
+ * hipStream_t (NULL = default stream).  Calls are asynchronous on `stream` and return a
+ * status (0 = KMOE_OK, negative = error; kmoe_strerror / kmoe_last_error describe it).
+ * Arguments are validated on the host before anything is launched.  Every entry point is
+ * re-entrant: layer handles are immutable after creation, and all scratch memory is a
+ * caller-provided workspace (calls that overlap on one workspace race).
+ *
+ * Weight layout (MLX affine quantization, group size 64), per projection stack:
+ *   weight  uint32 [E][rows][in*bits/32]  codes as a little-endian bit stream
+ *   scales  fp16|bf16 [E][rows][in/64]
+ *   biases  fp16|bf16 [E][rows][in/64]      w = q*scale + bias
+ * with gate/up rows = intermediate, in = hidden, and down rows = hidden, in = intermediate.
+ * The expert strides are explicit, so both mlx_lm's stacked SwitchGLU tensors and a
+ * BKEX file body uploaded as-is (kandiga/_pack_experts.py:6-20) can be described.
+ */
+#ifndef KANDIGA_AMD_H
+#define KANDIGA_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum kmoe_status {
+  KMOE_OK = 0,
+  KMOE_ERR_INVALID_ARG = -1,
+  KMOE_ERR_UNSUPPORTED = -2,
+  KMOE_ERR_ALIGNMENT = -3,
+  KMOE_ERR_WORKSPACE = -4,
+  KMOE_ERR_HIP = -5,
+  KMOE_ERR_IO = -6,
+  KMOE_ERR_FORMAT = -7,
+  KMOE_ERR_DEVICE = -8,
+  KMOE_ERR_NO_MEMORY = -9
+};
+
+enum { KMOE_SCALE_F16 = 0, KMOE_SCALE_BF16 = 1 };
+enum { KMOE_ACT_SWIGLU = 0, KMOE_ACT_GELU_TANH = 1 };
+enum { KMOE_PROJ_GATE = 0, KMOE_PROJ_UP = 1, KMOE_PROJ_DOWN = 2 };
+enum { KMOE_OUT_F16 = 0, KMOE_OUT_F32 = 1 };
+/* Device error flags reported by kmoe_device_status. */
+enum { KMOE_DEVERR_BAD_EXPERT = 1 };
+
+typedef struct {
+  const void* weight;            /* device, 16-byte aligned (4-bit) / 4-byte aligned (3-bit) */
+  const void* scales;            /* device, 2-byte aligned */
+  const void* biases;            /* device, 2-byte aligned */
+  int64_t weight_expert_stride;  /* bytes between consecutive experts' codes */
+  int64_t scale_expert_stride;   /* bytes between consecutive experts' scales (same for biases) */
+} kmoe_qproj;
+
+typedef struct {
+  int32_t hidden;        /* H, multiple of 64 */
+  int32_t intermediate;  /* I, multiple of 64 */
+  int32_t num_experts;   /* E, 1..1024 */
+  int32_t top_k;         /* K, 1..min(E, 16) */
+  int32_t bits;          /* 3 or 4 */
+  int32_t group_size;    /* must be 64 */
+  int32_t scale_dtype;   /* KMOE_SCALE_F16 or KMOE_SCALE_BF16 */
+  int32_t activation;    /* KMOE_ACT_SWIGLU (silu(g)*u) or KMOE_ACT_GELU_TANH */
+  kmoe_qproj gate, up, down;
+  /* Optional always-on dense fp16 shared expert added after the routed combine
+     (ungated): gate/up [Is][H], down [H][Is].  All NULL when absent. */
+  const void* shared_gate;
+  const void* shared_up;
+  const void* shared_down;
+  int32_t shared_intermediate;
+  int32_t reserved;
+} kmoe_layer_desc;
+
+typedef struct kmoe_layer kmoe_layer;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int kmoe_version(void);
+const char* kmoe_strerror(int status);
+/* Message of the last failing call on this thread ("" if none). */
+const char* kmoe_last_error(void);
+
+/* Validate a layer description and keep a copy (no device memory is allocated). */
+int kmoe_layer_create(const kmoe_layer_desc* desc, kmoe_layer** out);
+int kmoe_layer_destroy(kmoe_layer* layer);
+
+/* Bytes of workspace needed for calls of up to max_tokens tokens on this layer.
+ * The first 256 bytes hold device status words: zero the workspace once after allocating it. */
+int kmoe_workspace_size(const kmoe_layer* layer, int32_t max_tokens, size_t* bytes);
+
+/*
+ * Router: per token the top_k experts by router logit (ties -> lower index) and their
+ * softmax probabilities renormalised over the selected experts.
+ * Replaces router_softmax_topk (kandiga/metal/moe_block.metal:419-505) and mlx_lm's
+ * softmax -> argpartition -> renorm feeding switch_mlp (kandiga/engine.py:1090-1139).
+ *   logits  device fp32 [tokens][num_experts];  idx device int32 [tokens][top_k];
+ *   weights device fp32 [tokens][top_k].
+ */
+int kmoe_route(const float* logits, int32_t tokens, int32_t num_experts, int32_t top_k, int32_t* idx,
+               float* weights, void* stream);
+
+/*
+ * Stable token -> expert permutation (kandiga/engine.py:407-418, the grouping of
+ * _gpu_prefill_experts): perm lists the assignment ids a = t*top_k + k sorted by
+ * (expert, a); counts/offsets are the per-expert histogram and its exclusive scan;
+ * unique lists the experts with a nonzero count in ascending order, num_unique[0] their
+ * number.  All output pointers are device memory:
+ *   perm [tokens*top_k], counts [num_experts], offsets [num_experts+1],
+ *   unique [num_experts], num_unique [1].
+ */
+int kmoe_permute_workspace_size(int32_t tokens, int32_t top_k, int32_t num_experts, size_t* bytes);
+int kmoe_permute(const int32_t* idx, int32_t tokens, int32_t top_k, int32_t num_experts, int32_t* perm,
+                 int32_t* counts, int32_t* offsets, int32_t* unique, int32_t* num_unique, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+/*
+ * switch_mlp contract: y[t][k] = expert idx[t][k] applied to x[t] (SwiGLU gate/up/down over
+ * the quantized experts), not combined.  Replaces _CPUSwitchGLU.__call__ (kandiga/engine.py:
+ * 670-739) and, per token, bakan_cpu_expert_mlp_f16 (kandiga/metal/kandiga_cpu_expert.h:61-68).
+ *   x device fp16 [tokens][H]; idx device int32 [tokens][top_k]; y device fp16 [tokens][top_k][H].
+ */
+int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, int32_t tokens, void* y,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Weighted combine of switch_mlp outputs: out[t] = sum_k weights[t][k] * y[t][k], fp32
+ * accumulation in k order, one fp16 rounding (moe_block.metal:515-539, blend_kernel).
+ *   y device fp16 [tokens][top_k][hidden]; weights device fp32 [tokens][top_k];
+ *   out device fp16 [tokens][hidden].
+ */
+int kmoe_combine(const void* y, const float* weights, int32_t tokens, int32_t top_k, int32_t hidden, void* out,
+                 void* stream);
+
+/*
+ * Whole routed layer: route -> permute -> expert MLP -> weighted combine (+ shared expert).
+ * The block the reference assembles from mlx_lm's SparseMoeBlock router and combine around
+ * _CPUSwitchGLU (kandiga/engine.py:1090-1139, 670-739); its all-in-one restatement is the
+ * MoE step of the unwired C/Metal engine (kandiga/metal/full_forward_lg.m:1316-1350,
+ * 1635-1735: router_softmax_topk, expert_mlp_fused, blend_kernel).
+ *   x device fp16 [tokens][H]; logits device fp32 [tokens][E];
+ *   out device [tokens][H], fp16 (out_dtype KMOE_OUT_F16) or fp32 (KMOE_OUT_F32);
+ *   idx_out / weights_out (device, optional, may be NULL) receive the routing.
+ * 1..8 tokens run the GEMV decode kernels, larger batches the grouped MFMA GEMM.
+ */
+int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
+                 int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/*
+ * Dequantization check: codes (uint8 [nrows][in]) and fp16 weights round(q*s + b)
+ * (uint16 bits [nrows][in]) of rows row0.. of one expert's projection, as the kernels
+ * unpack them.  Device output pointers.
+ */
+int kmoe_dequantize(const kmoe_layer* layer, int32_t proj, int32_t expert, int32_t row0, int32_t nrows,
+                    uint8_t* codes, uint16_t* weights_f16, void* stream);
+
+/* Synchronise `stream`, then read and clear the device error flags kept in `workspace`. */
+int kmoe_device_status(void* workspace, size_t workspace_bytes, int32_t* flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KANDIGA_AMD_H */

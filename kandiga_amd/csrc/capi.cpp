@@ -1,0 +1,376 @@
+// C ABI of libkandiga_amd.so: argument validation, workspace carve-up and dispatch.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "../../include/kandiga_amd.h"
+#include "kmoe_internal.h"
+
+using namespace kmoe;
+
+struct kmoe_layer {
+  LayerConfig cfg;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return KMOE_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(KMOE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int max_mtiles_for(int TK, int E) { return (TK + GEMM_BM - 1) / GEMM_BM + (E < TK ? E : TK); }
+
+// Carve the workspace for `T` tokens.  base == nullptr computes the size only.
+Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y32, size_t* total) {
+  Work w{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> char* {
+    char* p = base ? base + off : nullptr;
+    off += up256(bytes);
+    return p;
+  };
+  const size_t TK = (size_t)T * K;
+  const int ntiles = (int)((TK + PERM_TILE - 1) / PERM_TILE);
+  const int mmt = max_mtiles_for((int)TK, E);
+  w.scalars = reinterpret_cast<int32_t*>(take(64 * sizeof(int32_t)));
+  w.idx = reinterpret_cast<int32_t*>(take(TK * 4));
+  w.wts = reinterpret_cast<float*>(take(TK * 4));
+  w.perm = reinterpret_cast<int32_t*>(take(TK * 4));
+  w.local_rank = reinterpret_cast<int32_t*>(take(TK * 4));
+  w.tile_hist = reinterpret_cast<int32_t*>(take((size_t)ntiles * E * 4));
+  w.counts = reinterpret_cast<int32_t*>(take((size_t)E * 4));
+  w.offsets = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
+  w.unique = reinterpret_cast<int32_t*>(take((size_t)E * 4));
+  w.ustart = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
+  w.mt_expert = reinterpret_cast<int32_t*>(take((size_t)mmt * 4));
+  w.mt_row0 = reinterpret_cast<int32_t*>(take((size_t)mmt * 4));
+  w.mt_rows = reinterpret_cast<int32_t*>(take((size_t)mmt * 4));
+  w.act = reinterpret_cast<uint16_t*>(take(TK * I * 2 * 2));  // hi and lo planes
+  if (need_y32) w.y32 = reinterpret_cast<float*>(take(TK * H * 4));
+  if (Is > 0) {
+    w.shared_out = reinterpret_cast<float*>(take((size_t)T * H * 4));
+    w.shared_act = reinterpret_cast<uint16_t*>(take((size_t)T * Is * 2));
+  }
+  *total = off;
+  return w;
+}
+
+bool is_decode(int T, int K) { return T <= DEC_MAX_TOKENS && T * K <= DEC_MAX_ASSIGN; }
+
+Work layer_work(const kmoe_layer* L, char* base, int T, size_t* total) {
+  const LayerArgs& a = L->cfg.args;
+  return carve(base, T, L->cfg.top_k, a.E, a.H, a.I, a.sh_gate ? a.Is : 0, !is_decode(T, L->cfg.top_k), total);
+}
+
+int check_qproj(const kmoe_qproj& q, const char* name, int rows, int in, int bits, int E) {
+  if (!q.weight || !q.scales || !q.biases) return fail(KMOE_ERR_INVALID_ARG, "%s: null pointer", name);
+  const int64_t wbytes = (int64_t)rows * in * bits / 8;
+  const int64_t sbytes = (int64_t)rows * (in / 64) * 2;
+  const size_t walign = bits == 4 ? 16 : 4;
+  if (!aligned(q.weight, walign) || q.weight_expert_stride % (int64_t)walign)
+    return fail(KMOE_ERR_ALIGNMENT, "%s.weight must be %zu-byte aligned (pointer and expert stride)", name, walign);
+  if (!aligned(q.scales, 2) || !aligned(q.biases, 2) || q.scale_expert_stride % 2)
+    return fail(KMOE_ERR_ALIGNMENT, "%s scales/biases must be 2-byte aligned", name);
+  if (E > 1 && (q.weight_expert_stride < wbytes || q.scale_expert_stride < sbytes))
+    return fail(KMOE_ERR_INVALID_ARG, "%s: expert stride smaller than one expert's tensor", name);
+  if (q.weight_expert_stride < 0 || q.scale_expert_stride < 0)
+    return fail(KMOE_ERR_INVALID_ARG, "%s: negative expert stride", name);
+  return KMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kmoe_version(void) { return 100; }
+
+const char* kmoe_strerror(int status) {
+  switch (status) {
+    case KMOE_OK: return "ok";
+    case KMOE_ERR_INVALID_ARG: return "invalid argument";
+    case KMOE_ERR_UNSUPPORTED: return "unsupported configuration";
+    case KMOE_ERR_ALIGNMENT: return "misaligned pointer or stride";
+    case KMOE_ERR_WORKSPACE: return "workspace too small";
+    case KMOE_ERR_HIP: return "HIP runtime error";
+    case KMOE_ERR_IO: return "I/O error";
+    case KMOE_ERR_FORMAT: return "bad file format";
+    case KMOE_ERR_DEVICE: return "device-side check failed";
+    case KMOE_ERR_NO_MEMORY: return "out of memory";
+    default: return "unknown status";
+  }
+}
+
+const char* kmoe_last_error(void) { return g_last_error.c_str(); }
+
+int kmoe_layer_create(const kmoe_layer_desc* d, kmoe_layer** out) {
+  if (!d || !out) return fail(KMOE_ERR_INVALID_ARG, "null descriptor or output pointer");
+  *out = nullptr;
+  if (d->bits != 3 && d->bits != 4) return fail(KMOE_ERR_UNSUPPORTED, "bits must be 3 or 4 (got %d)", d->bits);
+  if (d->group_size != 64) return fail(KMOE_ERR_UNSUPPORTED, "group_size must be 64 (got %d)", d->group_size);
+  if (d->hidden <= 0 || d->hidden % 64 || d->hidden > 65536)
+    return fail(KMOE_ERR_UNSUPPORTED, "hidden must be a positive multiple of 64 up to 65536 (got %d)", d->hidden);
+  if (d->intermediate <= 0 || d->intermediate % 64 || d->intermediate > 65536)
+    return fail(KMOE_ERR_UNSUPPORTED, "intermediate must be a positive multiple of 64 (got %d)", d->intermediate);
+  if (d->num_experts < 1 || d->num_experts > 1024)
+    return fail(KMOE_ERR_UNSUPPORTED, "num_experts must be in [1, 1024] (got %d)", d->num_experts);
+  if (d->top_k < 1 || d->top_k > 16 || d->top_k > d->num_experts)
+    return fail(KMOE_ERR_INVALID_ARG, "top_k must be in [1, min(16, num_experts)] (got %d)", d->top_k);
+  if (d->scale_dtype != KMOE_SCALE_F16 && d->scale_dtype != KMOE_SCALE_BF16)
+    return fail(KMOE_ERR_INVALID_ARG, "unknown scale_dtype %d", d->scale_dtype);
+  if (d->activation != KMOE_ACT_SWIGLU && d->activation != KMOE_ACT_GELU_TANH)
+    return fail(KMOE_ERR_INVALID_ARG, "unknown activation %d", d->activation);
+  // decode stage-1 LDS: 8 tokens x H fp16 + chunk sums must fit in 160 KiB
+  if ((size_t)8 * (d->hidden / 32) * 68 > 160 * 1024)
+    return fail(KMOE_ERR_UNSUPPORTED, "hidden %d too large for the decode kernels", d->hidden);
+  int rc;
+  if ((rc = check_qproj(d->gate, "gate", d->intermediate, d->hidden, d->bits, d->num_experts))) return rc;
+  if ((rc = check_qproj(d->up, "up", d->intermediate, d->hidden, d->bits, d->num_experts))) return rc;
+  if ((rc = check_qproj(d->down, "down", d->hidden, d->intermediate, d->bits, d->num_experts))) return rc;
+  const bool any_shared = d->shared_gate || d->shared_up || d->shared_down;
+  if (any_shared) {
+    if (!d->shared_gate || !d->shared_up || !d->shared_down)
+      return fail(KMOE_ERR_INVALID_ARG, "shared expert needs gate, up and down pointers");
+    if (d->shared_intermediate <= 0 || d->shared_intermediate % 64)
+      return fail(KMOE_ERR_INVALID_ARG, "shared_intermediate must be a positive multiple of 64");
+    if (!aligned(d->shared_gate, 16) || !aligned(d->shared_up, 16) || !aligned(d->shared_down, 16))
+      return fail(KMOE_ERR_ALIGNMENT, "shared expert weights must be 16-byte aligned");
+    return fail(KMOE_ERR_UNSUPPORTED, "shared expert not available in this build");
+  }
+  kmoe_layer* L = new (std::nothrow) kmoe_layer;
+  if (!L) return fail(KMOE_ERR_NO_MEMORY, "out of host memory");
+  LayerArgs& a = L->cfg.args;
+  auto qp = [](const kmoe_qproj& q) {
+    return QProj{static_cast<const uint8_t*>(q.weight), static_cast<const uint16_t*>(q.scales),
+                 static_cast<const uint16_t*>(q.biases), q.weight_expert_stride, q.scale_expert_stride / 2};
+  };
+  a.gate = qp(d->gate);
+  a.up = qp(d->up);
+  a.down = qp(d->down);
+  a.sh_gate = static_cast<const uint16_t*>(d->shared_gate);
+  a.sh_up = static_cast<const uint16_t*>(d->shared_up);
+  a.sh_down = static_cast<const uint16_t*>(d->shared_down);
+  a.H = d->hidden;
+  a.I = d->intermediate;
+  a.E = d->num_experts;
+  a.Is = any_shared ? d->shared_intermediate : 0;
+  L->cfg.top_k = d->top_k;
+  L->cfg.bits = d->bits;
+  L->cfg.bf16_scales = d->scale_dtype == KMOE_SCALE_BF16;
+  L->cfg.act = d->activation;
+  *out = L;
+  return ok();
+}
+
+int kmoe_layer_destroy(kmoe_layer* layer) {
+  delete layer;
+  return ok();
+}
+
+int kmoe_workspace_size(const kmoe_layer* layer, int32_t max_tokens, size_t* bytes) {
+  if (!layer || !bytes) return fail(KMOE_ERR_INVALID_ARG, "null layer or output pointer");
+  if (max_tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "max_tokens must be >= 0");
+  size_t total = 0, t2 = 0;
+  layer_work(layer, nullptr, max_tokens, &total);
+  // a call with fewer tokens may take the other path; size for both
+  if (max_tokens > 0) {
+    const int t_small = max_tokens < DEC_MAX_TOKENS ? max_tokens : DEC_MAX_TOKENS;
+    layer_work(layer, nullptr, t_small, &t2);
+    const LayerArgs& a = layer->cfg.args;
+    size_t t3 = 0;
+    carve(nullptr, max_tokens, layer->cfg.top_k, a.E, a.H, a.I, a.sh_gate ? a.Is : 0, true, &t3);
+    total = total > t3 ? total : t3;
+  }
+  *bytes = total > t2 ? total : t2;
+  return ok();
+}
+
+int kmoe_route(const float* logits, int32_t tokens, int32_t num_experts, int32_t top_k, int32_t* idx, float* weights,
+               void* stream) {
+  if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
+  if (num_experts < 1 || num_experts > 1024) return fail(KMOE_ERR_UNSUPPORTED, "num_experts must be in [1, 1024]");
+  if (top_k < 1 || top_k > 16 || top_k > num_experts)
+    return fail(KMOE_ERR_INVALID_ARG, "top_k must be in [1, min(16, num_experts)]");
+  if (tokens == 0) return ok();
+  if (!logits || !idx || !weights) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
+  if (!aligned(logits, 4) || !aligned(idx, 4) || !aligned(weights, 4))
+    return fail(KMOE_ERR_ALIGNMENT, "logits/idx/weights must be 4-byte aligned");
+  hipError_t e = launch_route(logits, tokens, num_experts, top_k, idx, weights, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "route launch");
+}
+
+int kmoe_permute_workspace_size(int32_t tokens, int32_t top_k, int32_t num_experts, size_t* bytes) {
+  if (!bytes || tokens < 0 || top_k < 1 || num_experts < 1 || num_experts > 1024)
+    return fail(KMOE_ERR_INVALID_ARG, "bad permutation size arguments");
+  size_t total = 0;
+  carve(nullptr, tokens, top_k, num_experts, 0, 0, 0, false, &total);
+  *bytes = total;
+  return ok();
+}
+
+int kmoe_permute(const int32_t* idx, int32_t tokens, int32_t top_k, int32_t num_experts, int32_t* perm,
+                 int32_t* counts, int32_t* offsets, int32_t* unique, int32_t* num_unique, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  if (tokens < 0 || top_k < 1 || top_k > 16 || num_experts < 1 || num_experts > 1024)
+    return fail(KMOE_ERR_INVALID_ARG, "bad permutation size arguments");
+  if (!counts || !offsets || !unique || !num_unique || !workspace)
+    return fail(KMOE_ERR_INVALID_ARG, "null pointer");
+  if (tokens > 0 && (!idx || !perm)) return fail(KMOE_ERR_INVALID_ARG, "null idx or perm");
+  size_t need = 0;
+  Work w = carve(static_cast<char*>(workspace), tokens, top_k, num_experts, 0, 0, 0, false, &need);
+  if (workspace_bytes < need)
+    return fail(KMOE_ERR_WORKSPACE, "workspace has %zu bytes, needs %zu", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  w.perm = perm;
+  w.counts = counts;
+  w.offsets = offsets;
+  w.unique = unique;
+  const int TK = tokens * top_k;
+  hipError_t e;
+  if (TK == 0) {
+    e = hipMemsetAsync(counts, 0, (size_t)num_experts * 4, s);
+    if (e == hipSuccess) e = hipMemsetAsync(offsets, 0, (size_t)(num_experts + 1) * 4, s);
+    if (e == hipSuccess) e = hipMemsetAsync(num_unique, 0, 4, s);
+    return e == hipSuccess ? ok() : hip_fail(e, "permute (empty)");
+  }
+  e = launch_permute(idx, TK, top_k, num_experts, w, max_mtiles_for(TK, num_experts), s);
+  if (e == hipSuccess) e = hipMemcpyAsync(num_unique, w.scalars, 4, hipMemcpyDeviceToDevice, s);
+  return e == hipSuccess ? ok() : hip_fail(e, "permute launch");
+}
+
+int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, int32_t tokens, void* y,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (!layer) return fail(KMOE_ERR_INVALID_ARG, "null layer");
+  if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
+  if (tokens == 0) return ok();
+  if (!x || !idx || !y || !workspace) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
+  if (!aligned(x, 16) || !aligned(y, 16) || !aligned(idx, 4))
+    return fail(KMOE_ERR_ALIGNMENT, "x and y must be 16-byte aligned, idx 4-byte aligned");
+  size_t need = 0;
+  Work w = layer_work(layer, static_cast<char*>(workspace), tokens, &need);
+  if (workspace_bytes < need) return fail(KMOE_ERR_WORKSPACE, "workspace has %zu bytes, needs %zu", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const LayerConfig& c = layer->cfg;
+  const int K = c.top_k;
+  const uint16_t* xx = static_cast<const uint16_t*>(x);
+  uint16_t* yy = static_cast<uint16_t*>(y);
+  hipError_t e;
+  if (is_decode(tokens, K)) {
+    e = launch_group_small(idx, tokens, K, c.args.E, w.perm, w.ustart, w.unique, w.scalars, s);
+    if (e == hipSuccess) e = launch_decode(c, xx, tokens, w, yy, 0, false, s);
+  } else {
+    const int mmt = max_mtiles_for(tokens * K, c.args.E);
+    e = launch_permute(idx, tokens * K, K, c.args.E, w, mmt, s);
+    if (e == hipSuccess) e = launch_gemm(c, xx, tokens, w, mmt, yy, s);
+  }
+  return e == hipSuccess ? ok() : hip_fail(e, "expert_mlp launch");
+}
+
+int kmoe_combine(const void* y, const float* weights, int32_t tokens, int32_t top_k, int32_t hidden, void* out,
+                 void* stream) {
+  if (tokens < 0 || top_k < 1 || top_k > 16 || hidden <= 0 || hidden % 64)
+    return fail(KMOE_ERR_INVALID_ARG, "bad combine sizes");
+  if (tokens == 0) return ok();
+  if (!y || !weights || !out) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
+  if (!aligned(y, 8) || !aligned(out, 8) || !aligned(weights, 4))
+    return fail(KMOE_ERR_ALIGNMENT, "y/out must be 8-byte aligned, weights 4-byte aligned");
+  hipError_t e = launch_combine16(static_cast<const uint16_t*>(y), weights, tokens, top_k, hidden,
+                                  static_cast<uint16_t*>(out), static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "combine launch");
+}
+
+int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
+                 int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  if (!layer) return fail(KMOE_ERR_INVALID_ARG, "null layer");
+  if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
+  if (out_dtype != KMOE_OUT_F16 && out_dtype != KMOE_OUT_F32) return fail(KMOE_ERR_INVALID_ARG, "unknown out_dtype");
+  const int out32 = out_dtype == KMOE_OUT_F32;
+  if (tokens == 0) return ok();
+  if (!x || !logits || !out || !workspace) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
+  if (!aligned(x, 16) || !aligned(out, 16) || !aligned(logits, 4))
+    return fail(KMOE_ERR_ALIGNMENT, "x and out must be 16-byte aligned, logits 4-byte aligned");
+  if ((idx_out && !aligned(idx_out, 4)) || (weights_out && !aligned(weights_out, 4)))
+    return fail(KMOE_ERR_ALIGNMENT, "idx_out/weights_out must be 4-byte aligned");
+  size_t need = 0;
+  Work w = layer_work(layer, static_cast<char*>(workspace), tokens, &need);
+  if (workspace_bytes < need) return fail(KMOE_ERR_WORKSPACE, "workspace has %zu bytes, needs %zu", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const LayerConfig& c = layer->cfg;
+  const LayerArgs& a = c.args;
+  const int K = c.top_k;
+  if (idx_out) w.idx = idx_out;
+  if (weights_out) w.wts = weights_out;
+  const uint16_t* xx = static_cast<const uint16_t*>(x);
+  hipError_t e = hipSuccess;
+  if (a.sh_gate) e = launch_shared(c, xx, tokens, w, s);
+  if (e != hipSuccess) return hip_fail(e, "shared expert launch");
+  if (is_decode(tokens, K)) {
+    e = launch_route_group(logits, tokens, a.E, K, w.idx, w.wts, w.perm, w.ustart, w.unique, w.scalars, s);
+    if (e == hipSuccess) e = launch_decode(c, xx, tokens, w, out, out32, true, s);
+  } else {
+    const int mmt = max_mtiles_for(tokens * K, a.E);
+    e = launch_route(logits, tokens, a.E, K, w.idx, w.wts, s);
+    if (e == hipSuccess) e = launch_permute(w.idx, tokens * K, K, a.E, w, mmt, s);
+    if (e == hipSuccess) e = launch_gemm(c, xx, tokens, w, mmt, nullptr, s);
+    if (e == hipSuccess)
+      e = launch_combine(w.y32, w.wts, tokens, K, a.H, a.sh_gate ? w.shared_out : nullptr, out, out32, s);
+  }
+  return e == hipSuccess ? ok() : hip_fail(e, "forward launch");
+}
+
+int kmoe_dequantize(const kmoe_layer* layer, int32_t proj, int32_t expert, int32_t row0, int32_t nrows,
+                    uint8_t* codes, uint16_t* weights_f16, void* stream) {
+  if (!layer || !codes || !weights_f16) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
+  if (proj < 0 || proj > 2) return fail(KMOE_ERR_INVALID_ARG, "proj must be 0 (gate), 1 (up) or 2 (down)");
+  const LayerArgs& a = layer->cfg.args;
+  const int rows = proj == 2 ? a.H : a.I;
+  if (expert < 0 || expert >= a.E) return fail(KMOE_ERR_INVALID_ARG, "expert %d out of range", expert);
+  if (row0 < 0 || nrows < 0 || row0 + nrows > rows) return fail(KMOE_ERR_INVALID_ARG, "row range out of bounds");
+  hipError_t e = launch_dequantize(layer->cfg, proj, expert, row0, nrows, codes, weights_f16,
+                                   static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "dequantize launch");
+}
+
+int kmoe_device_status(void* workspace, size_t workspace_bytes, int32_t* flags, void* stream) {
+  if (!workspace || !flags || workspace_bytes < 256) return fail(KMOE_ERR_INVALID_ARG, "bad workspace or flags");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int32_t* sc = static_cast<int32_t*>(workspace);
+  hipError_t e = hipMemcpyAsync(flags, sc + 2, 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e == hipSuccess) e = hipMemsetAsync(sc + 2, 0, 4, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return e == hipSuccess ? ok() : hip_fail(e, "device status");
+}
+
+}  // extern "C"
+
+namespace kmoe {
+hipError_t launch_shared(const LayerConfig&, const uint16_t*, int, const Work&, hipStream_t) {
+  return hipErrorNotSupported;
+}
+}  // namespace kmoe

@@ -1,0 +1,209 @@
+// Device-side building blocks shared by every kernel of the routed-expert layer (gfx950).
+//
+// Chunks and pair order
+// ---------------------
+// Quantized rows are processed in chunks of 32 codes: 12 bytes (3 dwords) for 3-bit
+// codes, 16 bytes (4 dwords) for 4-bit codes, both dword aligned.  A chunk is unpacked
+// into 16 "pairs": a 32-bit word whose low half holds one code and whose high half
+// holds another, each in bits 0..2 (3-bit) / 0..3 (4-bit) of its half.  The pair order
+// is chosen so that unpacking is a packed 16-bit shift plus one mask per pair (see
+// unpack3/unpack4 below); since a dot product is a sum, the activations only have to be
+// stored in the same order ("pair order") for the products to line up.  Activation
+// vectors handed between kernels (x staged in LDS, the SwiGLU output `act`) are stored
+// per 32-element chunk in pair order: position 2p holds element pair_lo(p) and
+// position 2p+1 holds element pair_hi(p).
+//
+// A pair word is used in one of two ways:
+//   * raw:   the half-words are fp16 subnormals q * 2^-24; v_dot2_f32_f16 against fp16
+//            activations accumulates exact products q*x*2^-24 in fp32, and the group
+//            scale/bias are applied once per 32 columns: s*2^24*dot + b*sum(x).
+//   * magic: OR 0x6400 gives the fp16 value 1024+q; subtracting 1024 gives q exactly and
+//            one fp16 fma gives the dequantized weight round(q*s + b) (MFMA operands).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace kmoe {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int GROUP = 64;
+constexpr int CHUNK = 32;  // codes per chunk
+
+template <int BITS>
+struct Bits {
+  static constexpr int chunk_bytes = BITS * 4;       // 12 or 16
+  static constexpr int chunk_dwords = BITS;           // 3 or 4
+  static constexpr uint32_t mask = BITS == 3 ? 0x00070007u : 0x000F000Fu;
+};
+
+// Pair tables: element index (0..31 within the chunk) of the low / high half of pair p.
+//   3-bit: (0,6)(1,7)(2,8)(3,9)(11,16)(12,17)(13,18)(14,19)(15,20)(22,27)(23,28)(24,29)
+//          (25,30)(4,31)(5,26)(10,21)
+//   4-bit: (8j+i, 8j+i+4) for j = 0..3, i = 0..3
+__host__ __device__ constexpr int pair_lo(int bits, int p) {
+  return bits == 3 ? (p < 4 ? p : p < 9 ? p + 7 : p < 13 ? p + 13 : p == 13 ? 4 : p == 14 ? 5 : 10)
+                   : 8 * (p >> 2) + (p & 3);
+}
+__host__ __device__ constexpr int pair_hi(int bits, int p) {
+  return bits == 3 ? (p < 4 ? p + 6 : p < 9 ? p + 12 : p < 13 ? p + 18 : p == 13 ? 31 : p == 14 ? 26 : 21)
+                   : 8 * (p >> 2) + (p & 3) + 4;
+}
+// Storage position (0..31) of element e of a chunk in pair order.
+__host__ __device__ constexpr int pair_pos(int bits, int e) {
+  int pos = 0;
+  for (int p = 0; p < 16; ++p) {
+    if (pair_lo(bits, p) == e) pos = 2 * p;
+    if (pair_hi(bits, p) == e) pos = 2 * p + 1;
+  }
+  return pos;
+}
+
+__device__ __forceinline__ uint32_t pk_shr(uint32_t v, unsigned lo, unsigned hi) {
+  u16x2_t x = __builtin_bit_cast(u16x2_t, v);
+  u16x2_t s = {(unsigned short)lo, (unsigned short)hi};
+  return __builtin_bit_cast(uint32_t, x >> s);
+}
+
+// v_perm_b32: result byte i = byte sel_i of {S1 bytes 0..3, S0 bytes 4..7}.
+__device__ __forceinline__ uint32_t perm_b32(uint32_t s0, uint32_t s1, uint32_t sel) {
+  return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
+// 3-bit chunk (dwords d0..d2, codes c_j at bits 3j of the 96-bit stream) -> 16 pairs.
+template <bool MAGIC>
+__device__ __forceinline__ void unpack3(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t (&p)[16]) {
+  constexpr uint32_t M = 0x00070007u, O = MAGIC ? 0x64006400u : 0u;
+  p[0] = (pk_shr(d0, 0, 2) & M) | O;
+  p[1] = (pk_shr(d0, 3, 5) & M) | O;
+  p[2] = (pk_shr(d0, 6, 8) & M) | O;
+  p[3] = (pk_shr(d0, 9, 11) & M) | O;
+  p[4] = (pk_shr(d1, 1, 0) & M) | O;
+  p[5] = (pk_shr(d1, 4, 3) & M) | O;
+  p[6] = (pk_shr(d1, 7, 6) & M) | O;
+  p[7] = (pk_shr(d1, 10, 9) & M) | O;
+  p[8] = (pk_shr(d1, 13, 12) & M) | O;
+  p[9] = (pk_shr(d2, 2, 1) & M) | O;
+  p[10] = (pk_shr(d2, 5, 4) & M) | O;
+  p[11] = (pk_shr(d2, 8, 7) & M) | O;
+  p[12] = (pk_shr(d2, 11, 10) & M) | O;
+  // c4: d0 bits 12..14 (low half); c31: d2 bits 29..31 (high half, relative 13)
+  p[13] = (pk_shr((d0 & 0xFFFFu) | (d2 & 0xFFFF0000u), 12, 13) & M) | O;
+  // c5: d0 bits 15..17; c26: d2 bits 14..16.  Bytes [d0.b1 d0.b2 | d2.b1 d2.b2] put them at 7 / 6.
+  p[14] = (pk_shr(perm_b32(d2, d0, 0x06050201u), 7, 6) & M) | O;
+  // c10: stream bits 30..32; c21: stream bits 63..65.
+  const uint32_t c10 = __builtin_amdgcn_alignbit(d1, d0, 30);
+  const uint32_t c21 = __builtin_amdgcn_alignbit(d2, d1, 31);
+  p[15] = (perm_b32(c21, c10, 0x05040100u) & M) | O;
+}
+
+// 4-bit chunk (dwords d0..d3, nibble n of dword j = code 8j+n) -> 16 pairs.
+template <bool MAGIC>
+__device__ __forceinline__ void unpack4(const uint32_t (&d)[4], uint32_t (&p)[16]) {
+  constexpr uint32_t M = 0x000F000Fu, O = MAGIC ? 0x64006400u : 0u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[4 * j + i] = ((d[j] >> (4 * i)) & M) | O;
+  }
+}
+
+template <int BITS, bool MAGIC>
+__device__ __forceinline__ void unpack_chunk(const uint32_t (&d)[4], uint32_t (&p)[16]) {
+  if constexpr (BITS == 3) {
+    unpack3<MAGIC>(d[0], d[1], d[2], p);
+  } else {
+    unpack4<MAGIC>(d, p);
+  }
+}
+
+// Load one chunk of packed codes (3 or 4 dwords; the address is dword aligned).
+template <int BITS>
+__device__ __forceinline__ void load_chunk(const uint8_t* __restrict__ row, int chunk, uint32_t (&d)[4]) {
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(row + (size_t)chunk * Bits<BITS>::chunk_bytes);
+  if constexpr (BITS == 3) {
+    d[0] = __builtin_nontemporal_load(src + 0);
+    d[1] = __builtin_nontemporal_load(src + 1);
+    d[2] = __builtin_nontemporal_load(src + 2);
+    d[3] = 0;
+  } else {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src));
+    d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+  }
+}
+
+// Permute 32 natural-order fp16 values (16 dwords, dword m = elements 2m, 2m+1) into pair order.
+template <int BITS>
+__device__ __forceinline__ void to_pair_order(const uint32_t (&nat)[16], uint32_t (&out)[16]) {
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+    const int lo = pair_lo(BITS, p), hi = pair_hi(BITS, p);
+    const uint32_t sel_lo = (lo & 1) ? 0x0302u : 0x0100u;        // bytes of S1 (low half source)
+    const uint32_t sel_hi = (hi & 1) ? 0x07060000u : 0x05040000u; // bytes of S0 (high half source)
+    out[p] = perm_b32(nat[hi >> 1], nat[lo >> 1], sel_hi | sel_lo);
+  }
+}
+
+__device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c, false);
+}
+
+// Sum of the 16 pair-dot products of a raw code chunk with an activation chunk (both pair order).
+__device__ __forceinline__ float chunk_dot(const uint32_t (&codes)[16], const uint32_t (&x)[16]) {
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int p = 0; p < 16; p += 2) {
+    a0 = fdot2(codes[p], x[p], a0);
+    a1 = fdot2(codes[p + 1], x[p + 1], a1);
+  }
+  return a0 + a1;
+}
+
+template <bool BF16>
+__device__ __forceinline__ float scale_to_f32(uint16_t v) {
+  if constexpr (BF16) {
+    return __uint_as_float((uint32_t)v << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, v);
+  }
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t v) {
+  return (float)__builtin_bit_cast(_Float16, v);
+}
+
+// Dequantize a magic pair word (each half 0x6400|q) to fp16 weights round(q*s + b).
+__device__ __forceinline__ uint32_t dequant_pair(uint32_t magic_pair, half2_t s2, half2_t b2) {
+  const half2_t q = __builtin_bit_cast(half2_t, magic_pair) - (half2_t){(_Float16)1024.0f, (_Float16)1024.0f};
+  return __builtin_bit_cast(uint32_t, q * s2 + b2);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+__device__ __forceinline__ float group_sum(float v, int width) {
+  for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+
+__device__ __forceinline__ float gelu_tanh_f32(float g) {
+  const float t = 0.7978845608f * (g + 0.044715f * g * g * g);
+  return 0.5f * g * (1.0f + tanhf(t));
+}
+
+}  // namespace kmoe

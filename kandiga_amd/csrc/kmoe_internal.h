@@ -1,0 +1,86 @@
+// Internal host/device interface between the C ABI (capi.cpp) and the kernel files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace kmoe {
+
+// One quantized projection stack: expert e, row r starts at
+//   w + e*w_stride + r*(in*bits/8)  and  s/b + e*s_stride + r*(in/64)  (strides in elements / bytes).
+struct QProj {
+  const uint8_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  int64_t w_stride;  // bytes
+  int64_t s_stride;  // uint16 elements
+};
+
+struct LayerArgs {
+  QProj gate, up, down;
+  const uint16_t* sh_gate;  // dense fp16 shared expert [Is][H] (or null)
+  const uint16_t* sh_up;    // [Is][H]
+  const uint16_t* sh_down;  // [H][Is]
+  int H, I, E, Is;
+};
+
+struct LayerConfig {
+  LayerArgs args;
+  int top_k;
+  int bits;
+  int bf16_scales;
+  int act;  // 0 SwiGLU, 1 GELU-tanh gate
+};
+
+// Workspace carve-up for one call (all pointers device memory, null when unused).
+struct Work {
+  int32_t* idx;        // [T*K]
+  float* wts;          // [T*K]
+  int32_t* perm;       // [T*K]   assignment ids sorted by (expert, id)
+  int32_t* local_rank; // [T*K]
+  int32_t* tile_hist;  // [ntiles][E]
+  int32_t* counts;     // [E]
+  int32_t* offsets;    // [E+1]
+  int32_t* unique;     // [E]
+  int32_t* ustart;     // [E+1]   group starts of the unique experts
+  int32_t* scalars;    // [0]=num_unique [1]=num GEMM m-tiles [2]=device error flags
+  int32_t* mt_expert;  // [max_mtiles]
+  int32_t* mt_row0;    // [max_mtiles]
+  int32_t* mt_rows;    // [max_mtiles]
+  uint16_t* act;       // 2 planes [T*K][I] fp16 (hi, lo), pair order, sorted rows
+  float* y32;          // [T*K][H] fp32 per-assignment expert outputs (GEMM path)
+  float* shared_out;     // [T][H] fp32 dense shared-expert output
+  uint16_t* shared_act;  // [T][Is] fp16 (pair order) shared-expert SwiGLU output
+};
+
+constexpr int PERM_TILE = 1024;   // assignments per permutation tile
+constexpr int GEMM_BM = 128;      // assignment rows per grouped-GEMM tile
+constexpr int DEC_MAX_TOKENS = 8; // largest batch served by the GEMV path
+constexpr int DEC_MAX_ASSIGN = 256;
+
+// Device error flag bits (Work::scalars[2]).
+constexpr int DEVERR_BAD_EXPERT = 1;
+
+// ---- launchers (return hipError_t of the launch) ----------------------------------------
+hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s);
+hipError_t launch_route_group(const float* logits, int T, int E, int K, int32_t* idx, float* wts,
+                              int32_t* perm, int32_t* ustart, int32_t* unique, int32_t* scalars, hipStream_t s);
+hipError_t launch_group_small(const int32_t* idx, int T, int K, int E, int32_t* perm, int32_t* ustart,
+                              int32_t* unique, int32_t* scalars, hipStream_t s);
+hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, hipStream_t s);
+
+hipError_t launch_decode(const LayerConfig& c, const uint16_t* x, int T, const Work& w, void* out, int out32,
+                         bool combine, hipStream_t s);
+hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Work& w, int max_mtiles,
+                       uint16_t* y16, hipStream_t s);
+hipError_t launch_combine(const float* y32, const float* wts, int T, int K, int H, const float* shared,
+                          void* out, int out32, hipStream_t s);
+hipError_t launch_combine16(const uint16_t* y16, const float* wts, int T, int K, int H, uint16_t* out,
+                            hipStream_t s);
+hipError_t launch_shared(const LayerConfig& c, const uint16_t* x, int T, const Work& w, hipStream_t s);
+hipError_t launch_dequantize(const LayerConfig& c, int proj, int expert, int row0, int nrows, uint8_t* codes,
+                             uint16_t* wf16, hipStream_t s);
+
+size_t decode_lds_bytes(const LayerConfig& c, int T);
+
+}  // namespace kmoe

@@ -1,0 +1,319 @@
+"""Host side of the routed-expert MoE layer: torch tensors in HBM, HIP kernels via the C ABI.
+
+Mirrors the reference's operator interface for this path:
+
+* :class:`QuantizedSwitchGLU` -- drop-in for ``_CPUSwitchGLU`` / mlx_lm ``SwitchGLU``
+  (kandiga/engine.py:327-739): ``__call__(x [..., H], indices [..., K]) -> y [..., K, H]``,
+  the per-(token, k) expert outputs, not combined, fp16.
+* :class:`SparseMoeBlock` -- the routed block around it (router softmax -> top-K ->
+  renorm, switch_mlp, weighted combine; mlx_lm's SparseMoeBlock as driven by
+  engine.py:1090-1139, restated in kandiga/metal/moe_block.metal:419-584) with the router
+  logits as input: ``__call__(x [..., H], logits [..., E]) -> out [..., H]``.
+* :func:`route`, :func:`permute`, :func:`combine` -- the individual stages.
+
+Errors raise :class:`~kandiga_amd._capi.KmoeError` (the reference raises RuntimeError on a
+nonzero status, engine.py:185-186); a missing library raises ImportError.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _capi
+from .layout import GROUP_SIZE, ExpertGeometry, read_bkex_header, BKEX_HEADER_SIZE
+from .synth import LayerShape
+
+_PROJS = ("gate", "up", "down")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _as_u16(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.int16) if t.dtype in (torch.float16, torch.bfloat16, torch.int16, torch.uint16) else t
+
+
+@dataclass
+class _Proj:
+    weight: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+    weight_stride: int   # bytes between experts
+    scale_stride: int    # bytes between experts
+
+
+class QuantizedExperts:
+    """All experts of one layer resident in device memory (MLX affine layout, group 64).
+
+    Holds the ``kmoe_layer`` handle and a workspace that grows with the largest token
+    count seen (allocate it up front with :meth:`reserve` to keep allocation out of
+    timed regions).
+    """
+
+    def __init__(self, shape: LayerShape, projs: dict, scale_dtype: str = "f16", activation: str = "swiglu",
+                 shared: dict | None = None, keepalive=None):
+        if scale_dtype not in ("f16", "bf16"):
+            raise ValueError("scale_dtype must be 'f16' or 'bf16'")
+        if activation not in ("swiglu", "gelu_tanh"):
+            raise ValueError("activation must be 'swiglu' or 'gelu_tanh'")
+        self.shape = shape
+        self.scale_dtype = scale_dtype
+        self.activation = activation
+        self.projs = projs
+        self.shared = shared
+        self._keepalive = keepalive
+        dev = projs["gate"].weight.device
+        if dev.type != "cuda":
+            raise ValueError("expert weights must be on a cuda (HIP) device")
+        self.device = dev
+        d = _capi.LayerDesc()
+        d.hidden, d.intermediate = shape.hidden, shape.intermediate
+        d.num_experts, d.top_k, d.bits, d.group_size = shape.num_experts, shape.top_k, shape.bits, GROUP_SIZE
+        d.scale_dtype = _capi.SCALE_BF16 if scale_dtype == "bf16" else _capi.SCALE_F16
+        d.activation = _capi.ACT_GELU_TANH if activation == "gelu_tanh" else _capi.ACT_SWIGLU
+        for name in _PROJS:
+            p = projs[name]
+            q = getattr(d, name)
+            q.weight, q.scales, q.biases = p.weight.data_ptr(), p.scales.data_ptr(), p.biases.data_ptr()
+            q.weight_expert_stride, q.scale_expert_stride = p.weight_stride, p.scale_stride
+        if shared:
+            d.shared_gate = shared["gate"].data_ptr()
+            d.shared_up = shared["up"].data_ptr()
+            d.shared_down = shared["down"].data_ptr()
+            d.shared_intermediate = shape.shared_intermediate
+        self._desc = d
+        L = _capi.lib()
+        h = ctypes.c_void_p()
+        _capi.check(L.kmoe_layer_create(ctypes.byref(d), ctypes.byref(h)), "kmoe_layer_create")
+        self._handle = h
+        self._ws = None
+        self._ws_tokens = -1
+
+    # ---- construction helpers ---------------------------------------------------------
+    @classmethod
+    def from_stacked(cls, shape: LayerShape, layer: dict, device="cuda", scale_dtype: str = "f16",
+                     activation: str = "swiglu") -> "QuantizedExperts":
+        """From a stacked layer dict (numpy from :func:`synth.make_layer` or torch tensors)."""
+        projs = {}
+        keep = []
+        for name in _PROJS:
+            ts = []
+            for key in ("w", "s", "b"):
+                a = layer[f"{name}_{key}"]
+                t = a if isinstance(a, torch.Tensor) else torch.from_numpy(a.view(a.dtype.str.replace("u", "i")))
+                t = t.to(device).contiguous()
+                ts.append(t)
+            w, s, b = ts
+            projs[name] = _Proj(w, _as_u16(s), _as_u16(b), w[0].numel() * w.element_size(),
+                                s[0].numel() * s.element_size())
+            keep += ts
+        shared = None
+        if shape.shared_intermediate and "shared_gate" in layer:
+            shared = {}
+            for name in _PROJS:
+                a = layer[f"shared_{name}"]
+                t = a if isinstance(a, torch.Tensor) else torch.from_numpy(a.view("i2"))
+                shared[name] = t.to(device).contiguous()
+        return cls(shape, projs, scale_dtype, activation, shared, keep)
+
+    @classmethod
+    def from_bkex(cls, path: str, top_k: int, device="cuda", activation: str | None = None) -> "QuantizedExperts":
+        """Load a BKEX ``layer_XX.bin`` file: the expert blocks are uploaded as one buffer and
+        described with the block size as expert stride (no repacking).  The activation
+        defaults to GELU-tanh for intermediate size 704 and SwiGLU otherwise, as the
+        header-driven reference does (kandiga/metal/kandiga_cpu_expert_lg.m:109-111)."""
+        hdr = read_bkex_header(path)
+        geom = ExpertGeometry(hdr.hidden, hdr.intermediate, hdr.bits)
+        import numpy as np
+        body = np.fromfile(path, dtype=np.uint8, offset=BKEX_HEADER_SIZE)
+        if body.size != hdr.num_experts * hdr.expert_size:
+            raise ValueError(f"{path}: truncated BKEX body")
+        buf = torch.from_numpy(body).to(device)
+        offs = geom.offsets()
+        shape = LayerShape(hdr.hidden, hdr.intermediate, hdr.num_experts, top_k, hdr.bits)
+        projs = {}
+        for name in _PROJS:
+            base = buf.data_ptr()
+            w = buf[offs[f"{name}_proj.weight"]:]
+            s = buf[offs[f"{name}_proj.scales"]:]
+            b = buf[offs[f"{name}_proj.biases"]:]
+            if (base + offs[f"{name}_proj.weight"]) % (16 if hdr.bits == 4 else 4):
+                raise ValueError("BKEX weight tensor is misaligned")
+            projs[name] = _Proj(w, s, b, hdr.expert_size, hdr.expert_size)
+        act = activation or ("gelu_tanh" if hdr.intermediate == 704 else "swiglu")
+        return cls(shape, projs, hdr.scale_dtype, act, None, [buf])
+
+    # ---- workspace --------------------------------------------------------------------
+    def workspace_bytes(self, tokens: int) -> int:
+        n = ctypes.c_size_t()
+        _capi.check(_capi.lib().kmoe_workspace_size(self._handle, int(tokens), ctypes.byref(n)),
+                    "kmoe_workspace_size")
+        return n.value
+
+    def reserve(self, tokens: int) -> None:
+        """Allocate (zeroed) workspace for calls of up to ``tokens`` tokens."""
+        if tokens > self._ws_tokens:
+            self._ws = torch.zeros(max(self.workspace_bytes(tokens), 256), dtype=torch.uint8, device=self.device)
+            self._ws_tokens = tokens
+
+    def workspace(self, tokens: int) -> torch.Tensor:
+        self.reserve(tokens)
+        return self._ws
+
+    def device_status(self) -> int:
+        """Read and clear the device error flags (synchronises the current stream)."""
+        if self._ws is None:
+            return 0
+        f = ctypes.c_int32()
+        _capi.check(_capi.lib().kmoe_device_status(self._ws.data_ptr(), self._ws.numel(), ctypes.byref(f),
+                                                   _stream()), "kmoe_device_status")
+        return f.value
+
+    def dequantize(self, proj: str, expert: int, row0: int = 0, nrows: int = 1):
+        """(codes uint8 [nrows, in], fp16 weights [nrows, in]) as the kernels unpack them."""
+        pi = _PROJS.index(proj)
+        in_dim = self.shape.intermediate if proj == "down" else self.shape.hidden
+        codes = torch.empty((nrows, in_dim), dtype=torch.uint8, device=self.device)
+        w16 = torch.empty((nrows, in_dim), dtype=torch.float16, device=self.device)
+        _capi.check(_capi.lib().kmoe_dequantize(self._handle, pi, expert, row0, nrows, codes.data_ptr(),
+                                                w16.data_ptr(), _stream()), "kmoe_dequantize")
+        return codes, w16
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and _capi._lib is not None:
+            _capi._lib.kmoe_layer_destroy(h)
+            self._handle = None
+
+
+def _check_x(x: torch.Tensor, H: int) -> torch.Tensor:
+    if x.shape[-1] != H:
+        raise ValueError(f"last dimension of x is {x.shape[-1]}, expected {H}")
+    if x.dtype == torch.bfloat16:
+        x = x.to(torch.float16)
+    if x.dtype != torch.float16:
+        raise TypeError(f"x must be float16 or bfloat16, got {x.dtype}")
+    return x.reshape(-1, H).contiguous()
+
+
+class QuantizedSwitchGLU:
+    """``switch_mlp(x, indices)``: per-(token, k) SwiGLU expert outputs ``[..., K, H]`` (fp16).
+
+    Same contract as the reference's ``_CPUSwitchGLU.__call__`` (kandiga/engine.py:670-739).
+    """
+
+    def __init__(self, experts: QuantizedExperts):
+        self.experts = experts
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        E = self.experts
+        K = indices.shape[-1]
+        if K != E.shape.top_k:
+            raise ValueError(f"indices have {K} experts per token, layer was built for top_k={E.shape.top_k}")
+        xf = _check_x(x, E.shape.hidden)
+        idx = indices.reshape(-1, K).to(torch.int32).contiguous()
+        T = xf.shape[0]
+        if idx.shape[0] != T:
+            raise ValueError("x and indices disagree on the number of tokens")
+        y = torch.empty((T, K, E.shape.hidden), dtype=torch.float16, device=E.device)
+        ws = E.workspace(T)
+        _capi.check(_capi.lib().kmoe_expert_mlp(E._handle, xf.data_ptr(), idx.data_ptr(), T, y.data_ptr(),
+                                                ws.data_ptr(), ws.numel(), _stream()), "kmoe_expert_mlp")
+        return y.reshape(*indices.shape, E.shape.hidden)
+
+
+class SparseMoeBlock:
+    """Routed MoE block: route(logits) -> switch_mlp -> weighted combine (+ shared expert)."""
+
+    def __init__(self, experts: QuantizedExperts):
+        self.experts = experts
+        self.switch_mlp = QuantizedSwitchGLU(experts)
+
+    @property
+    def top_k(self) -> int:
+        return self.experts.shape.top_k
+
+    def __call__(self, x: torch.Tensor, logits: torch.Tensor, return_routing: bool = False,
+                 out_dtype: torch.dtype = torch.float16):
+        """``out_dtype`` float16 (default) or float32 (the combine result before fp16 rounding)."""
+        E = self.experts
+        if out_dtype not in (torch.float16, torch.float32):
+            raise TypeError("out_dtype must be torch.float16 or torch.float32")
+        lead = x.shape[:-1]
+        xf = _check_x(x, E.shape.hidden)
+        lg = logits.reshape(-1, E.shape.num_experts).to(torch.float32).contiguous()
+        T = xf.shape[0]
+        if lg.shape[0] != T:
+            raise ValueError("x and logits disagree on the number of tokens")
+        out = torch.empty((T, E.shape.hidden), dtype=out_dtype, device=E.device)
+        idx = w = None
+        if return_routing:
+            idx = torch.empty((T, E.shape.top_k), dtype=torch.int32, device=E.device)
+            w = torch.empty((T, E.shape.top_k), dtype=torch.float32, device=E.device)
+        ws = E.workspace(T)
+        odt = _capi.OUT_F32 if out_dtype == torch.float32 else _capi.OUT_F16
+        _capi.check(_capi.lib().kmoe_forward(E._handle, xf.data_ptr(), lg.data_ptr(), T, out.data_ptr(), odt,
+                                             _ptr(idx), _ptr(w), ws.data_ptr(), ws.numel(), _stream()),
+                    "kmoe_forward")
+        out = out.reshape(*lead, E.shape.hidden)
+        if return_routing:
+            return out, idx.reshape(*lead, -1), w.reshape(*lead, -1)
+        return out
+
+
+def route(logits: torch.Tensor, top_k: int):
+    """Top-K experts per token (ties -> lower index) and renormalised softmax weights."""
+    lg = logits.to(torch.float32).contiguous()
+    T, E = lg.reshape(-1, lg.shape[-1]).shape
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=lg.device)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=lg.device)
+    _capi.check(_capi.lib().kmoe_route(lg.data_ptr(), T, E, top_k, idx.data_ptr(), w.data_ptr(), _stream()),
+                "kmoe_route")
+    lead = logits.shape[:-1]
+    return idx.reshape(*lead, top_k), w.reshape(*lead, top_k)
+
+
+def permute(idx: torch.Tensor, num_experts: int) -> dict:
+    """Stable token->expert grouping: perm, counts, offsets, unique experts (engine.py:407-418)."""
+    K = idx.shape[-1]
+    ii = idx.reshape(-1, K).to(torch.int32).contiguous()
+    T = ii.shape[0]
+    dev = ii.device
+    L = _capi.lib()
+    n = ctypes.c_size_t()
+    _capi.check(L.kmoe_permute_workspace_size(T, K, num_experts, ctypes.byref(n)), "kmoe_permute_workspace_size")
+    ws = torch.zeros(max(n.value, 256), dtype=torch.uint8, device=dev)
+    perm = torch.empty(T * K, dtype=torch.int32, device=dev)
+    counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    unique = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    nu = torch.empty(1, dtype=torch.int32, device=dev)
+    _capi.check(L.kmoe_permute(ii.data_ptr(), T, K, num_experts, perm.data_ptr(), counts.data_ptr(),
+                               offsets.data_ptr(), unique.data_ptr(), nu.data_ptr(), ws.data_ptr(), ws.numel(),
+                               _stream()), "kmoe_permute")
+    f = ctypes.c_int32()
+    _capi.check(L.kmoe_device_status(ws.data_ptr(), ws.numel(), ctypes.byref(f), _stream()), "kmoe_device_status")
+    if f.value & _capi.DEVERR_BAD_EXPERT:
+        raise _capi.KmoeError(_capi.ERR_DEVICE, "kmoe_permute: expert index out of range")
+    u = int(nu.item())
+    return dict(perm=perm, s_tok=perm // K, s_k=perm % K, counts=counts, offsets=offsets,
+                unique=unique[:u], num_unique=u)
+
+
+def combine(y: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
+    """``out[t] = sum_k w[t,k] * y[t,k]`` (fp32 accumulate, fp16 out) for y ``[..., K, H]`` fp16."""
+    K, H = y.shape[-2], y.shape[-1]
+    yy = y.reshape(-1, K, H).to(torch.float16).contiguous()
+    ww = weights.reshape(-1, K).to(torch.float32).contiguous()
+    T = yy.shape[0]
+    out = torch.empty((T, H), dtype=torch.float16, device=y.device)
+    _capi.check(_capi.lib().kmoe_combine(yy.data_ptr(), ww.data_ptr(), T, K, H, out.data_ptr(), _stream()),
+                "kmoe_combine")
+    return out.reshape(*y.shape[:-2], H)

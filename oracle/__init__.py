@@ -1,0 +1,18 @@
+"""ORACLE -- test infrastructure only.
+
+CPU restatements of the reference's routed-expert MoE layer, used as the checker by
+``tests/``, by ``__graft_entry__.smoke()`` and by the CPU-baseline leg of ``bench.py``.
+Nothing in the ``kandiga_amd`` package imports, links or calls this package; the
+product path runs only the HIP library and fails if it is missing.
+
+Pins (each function's docstring names its checks in ``tests/``):
+
+* ``unpack_codes``      known-answer byte patterns, pack/unpack round trip, the BKEX
+                        offset constants of kandiga_cpu_expert.m:42-65.
+* ``dequantize``        closed form ``(q - 2**(b-1)) * s`` exact for the synthetic scales.
+* ``route``             brute force over E on small inputs, softmax identities, tie cases.
+* ``permute``           brute-force ``sorted(range(T*K), key=(expert, flat index))``.
+* ``combine``           closed form ``sum_k w_k y_k``, linearity.
+* ``switch_mlp`` (C)    float64 numpy matmul over fully dequantized matrices
+                        (``expert_mlp_f64``), zero-weight and one-hot special cases.
+"""

@@ -1,0 +1,68 @@
+"""Shared helpers of the GPU parity tests (seeded layers, oracle subsets, error metrics)."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from kandiga_amd import synth
+from oracle import moe_oracle as O
+
+# Output tolerance of the routed layer against the fp32-accumulated oracle.
+MAX_ABS = 2e-2
+REL_L2 = 1e-3
+
+
+def f16_ulp(v: np.ndarray) -> np.ndarray:
+    """Spacing of fp16 values at |v| (normal range; 2**-24 below it)."""
+    a = np.abs(np.asarray(v, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return np.exp2(e - 10)
+
+
+def assert_close(got, ref, max_abs=MAX_ABS, rel_l2=REL_L2, what="", fp16_out=None):
+    """max |got-ref| <= max_abs and rel-L2 <= rel_l2.
+
+    For fp16 outputs (``got`` of dtype float16, or ``fp16_out=True``) an element may instead
+    be within one fp16 ulp of the fp32 reference: above |out| = 32 that spacing (1/32)
+    exceeds 2e-2 and no fp16 value can be closer.
+    """
+    is16 = (np.asarray(got).dtype == np.float16) if fp16_out is None else fp16_out
+    g = np.asarray(got, dtype=np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    err = O.compare(g, r)
+    diff = np.abs(g - r)
+    allowed = np.maximum(max_abs, f16_ulp(r)) if is16 else np.full_like(r, max_abs)
+    worst = float((diff - allowed).max()) if diff.size else 0.0
+    print(f"  {what}: max_abs={err['max_abs']:.3e} rel_l2={err['rel_l2']:.3e} max|ref|="
+          f"{float(np.abs(r).max()) if r.size else 0:.1f} fp16_out={is16}", flush=True)
+    assert worst <= 0 and err["rel_l2"] <= rel_l2, f"{what}: {err} (worst excess {worst:.3e})"
+    return err
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def torch_layer_subset(layer_t: dict, experts) -> dict:
+    """Host copy of the listed experts of a device-generated layer (oracle input)."""
+    ex = torch.as_tensor(np.asarray(experts, dtype=np.int64), device=layer_t["gate_w"].device)
+    out = {}
+    for k, v in layer_t.items():
+        if k.startswith("shared_"):
+            out[k] = to_np(v).view(np.uint16)
+            continue
+        sub = to_np(v.index_select(0, ex))
+        out[k] = sub.view(np.uint32) if k.endswith("_w") else sub.view(np.uint16)
+    return out
+
+
+def oracle_rows(layer_np: dict, x: np.ndarray, idx: np.ndarray, bits: int, scale_dtype="f16", nthreads=8):
+    """Oracle switch_mlp for the given tokens, on a layer that may be an expert subset:
+    ``idx`` holds positions into the subset."""
+    return O.switch_mlp(layer_np, x, idx, bits, scale_dtype, nthreads=nthreads)
+
+
+def remap(idx: np.ndarray):
+    """Distinct experts of idx and idx rewritten as positions into that list."""
+    uniq, inv = np.unique(idx, return_inverse=True)
+    return uniq, inv.reshape(idx.shape).astype(np.int32)

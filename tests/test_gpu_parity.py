@@ -1,0 +1,233 @@
+"""GPU parity of the HIP path (through the C ABI) against the oracle.
+
+Bit-exact: dequantized codes, top-K indices, permutation order, histogram.
+Tolerance (layer and switch_mlp outputs vs the fp32-accumulated oracle):
+max |err| <= 2e-2 and relative L2 <= 1e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+from kandiga_amd import synth
+from kandiga_amd.layout import unpack_codes
+from oracle import moe_oracle as O
+from tests.gpu_helpers import assert_close, to_np, remap, torch_layer_subset
+
+pytestmark = pytest.mark.gpu
+
+SMALL = {
+    "3bit": synth.LayerShape(256, 128, 16, 4, 3),
+    "4bit": synth.LayerShape(256, 128, 16, 4, 4),
+    "3bit-h320-i192": synth.LayerShape(320, 192, 12, 3, 3),
+}
+
+
+def _experts(shape, seed, device, scale_dtype="f16", activation="swiglu"):
+    from kandiga_amd.moe import QuantizedExperts
+
+    layer = synth.make_layer(shape, seed, scale_dtype)
+    return layer, QuantizedExperts.from_stacked(shape, layer, device, scale_dtype, activation)
+
+
+@pytest.mark.parametrize("name", sorted(SMALL))
+@pytest.mark.parametrize("scale_dtype", ["f16", "bf16"])
+def test_dequantize_bitexact(device, name, scale_dtype):
+    shape = SMALL[name]
+    layer, ex = _experts(shape, 11, device, scale_dtype)
+    for proj, rows, in_dim in (("gate", shape.intermediate, shape.hidden), ("up", shape.intermediate, shape.hidden),
+                               ("down", shape.hidden, shape.intermediate)):
+        for e in (0, shape.num_experts - 1):
+            codes, w16 = ex.dequantize(proj, e, 0, rows)
+            ref_codes = O.unpack_codes(layer[f"{proj}_w"][e], shape.bits, in_dim)
+            assert np.array_equal(to_np(codes), ref_codes), f"{proj} expert {e} codes differ"
+            ref_w = O.dequantize(layer[f"{proj}_w"][e], layer[f"{proj}_s"][e], layer[f"{proj}_b"][e], shape.bits,
+                                 in_dim, scale_dtype).astype(np.float16)
+            assert np.array_equal(to_np(w16).view(np.uint16), ref_w.view(np.uint16)), f"{proj} expert {e} weights"
+
+
+@pytest.mark.parametrize("E,K,T", [(16, 4, 5), (256, 8, 1), (256, 8, 333), (256, 4, 8), (512, 10, 67),
+                                   (64, 1, 3), (1000, 16, 9)])
+def test_route_bitexact(device, E, K, T):
+    from kandiga_amd.moe import route
+
+    rng = np.random.default_rng(E * 31 + K * 7 + T)
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    # ties: duplicated values, a row of equal logits, signed zeros, -inf
+    if T > 2:
+        logits[1, ::3] = logits[1, 0]
+        logits[2, :] = 0.25
+    logits[0, : min(E, 4)] = -np.inf
+    logits[0, min(E, 4):min(E, 8)] = [-0.0, 0.0, -0.0, 0.0][: max(0, min(E, 8) - min(E, 4))]
+    idx, w = route(torch.from_numpy(logits).to(device), K)
+    ref_idx, ref_w = O.route(logits, K)
+    assert np.array_equal(to_np(idx), ref_idx)
+    np.testing.assert_allclose(to_np(w), ref_w, rtol=2e-6, atol=2e-7)
+
+
+@pytest.mark.parametrize("T,K,E,zipf", [(1, 8, 256, False), (8, 8, 256, False), (512, 8, 256, True),
+                                        (4096, 8, 256, True), (333, 10, 512, False), (2000, 4, 7, False)])
+def test_permute_bitexact(device, T, K, E, zipf):
+    from kandiga_amd.moe import permute, route
+
+    shape = synth.LayerShape(64, 64, E, K, 3)
+    _x, logits = synth.make_inputs(shape, T, 5, zipf=zipf)
+    ref_idx, _ = O.route(logits, K)
+    got = permute(torch.from_numpy(ref_idx).to(device), E)
+    ref = O.permute(ref_idx, E)
+    assert np.array_equal(to_np(got["perm"]), ref["perm"])
+    assert np.array_equal(to_np(got["counts"]), ref["counts"])
+    assert np.array_equal(to_np(got["offsets"]), ref["offsets"])
+    assert np.array_equal(to_np(got["unique"]), ref["unique"])
+
+
+def test_permute_rejects_bad_index(device):
+    from kandiga_amd import _capi
+    from kandiga_amd.moe import permute
+
+    idx = torch.tensor([[0, 3], [9, 1]], dtype=torch.int32, device=device)
+    with pytest.raises(_capi.KmoeError):
+        permute(idx, 4)
+
+
+@pytest.mark.parametrize("name", sorted(SMALL))
+@pytest.mark.parametrize("T", [1, 3, 8, 40, 300])
+def test_switch_mlp_small(device, name, T):
+    from kandiga_amd.moe import QuantizedSwitchGLU
+
+    shape = SMALL[name]
+    layer, ex = _experts(shape, 21, device)
+    x, logits = synth.make_inputs(shape, T, 22)
+    idx, _w = O.route(logits, shape.top_k)
+    y = QuantizedSwitchGLU(ex)(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device))
+    assert ex.device_status() == 0
+    ref = O.switch_mlp(layer, x, idx, shape.bits)
+    assert_close(to_np(y), ref, what=f"{name} T={T} switch_mlp")
+
+
+@pytest.mark.parametrize("name", sorted(SMALL))
+@pytest.mark.parametrize("T", [1, 2, 5, 8, 9, 64, 700])
+def test_forward_small(device, name, T):
+    from kandiga_amd.moe import SparseMoeBlock
+
+    shape = SMALL[name]
+    layer, ex = _experts(shape, 31, device)
+    x, logits = synth.make_inputs(shape, T, 32, zipf=T > 50)
+    out, idx, w = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device),
+                                     return_routing=True)
+    ref = O.moe_layer(layer, x, logits, shape.top_k, shape.bits)
+    assert np.array_equal(to_np(idx), ref["idx"])
+    np.testing.assert_allclose(to_np(w), ref["w"], rtol=2e-6, atol=2e-7)
+    assert_close(to_np(out), ref["out"], what=f"{name} T={T} layer")
+    out32 = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device),
+                               out_dtype=torch.float32)
+    assert_close(to_np(out32), ref["out"], what=f"{name} T={T} layer fp32 out")
+
+
+def test_forward_bf16_scales_gelu(device):
+    from kandiga_amd.moe import SparseMoeBlock
+
+    shape = synth.LayerShape(256, 128, 16, 4, 3)
+    layer = synth.make_layer(shape, 41, "bf16")
+    from kandiga_amd.moe import QuantizedExperts
+
+    ex = QuantizedExperts.from_stacked(shape, layer, device, "bf16", "gelu_tanh")
+    for T in (2, 100):
+        x, logits = synth.make_inputs(shape, T, 42 + T)
+        out = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device))
+        idx, w = O.route(logits, shape.top_k)
+        y = O.switch_mlp(layer, x, idx, 3, "bf16", act="gelu")
+        assert_close(to_np(out), O.combine(y, w), what=f"bf16 gelu T={T}")
+
+
+def test_combine_matches_closed_form(device):
+    from kandiga_amd.moe import combine
+
+    rng = np.random.default_rng(3)
+    y = (rng.standard_normal((37, 6, 192)) * 3).astype(np.float16)
+    w = rng.random((37, 6)).astype(np.float32)
+    out = combine(torch.from_numpy(y).to(device), torch.from_numpy(w).to(device))
+    ref = O.combine(y.astype(np.float32), w)
+    np.testing.assert_allclose(to_np(out).astype(np.float32), ref, rtol=1e-3, atol=1e-3)
+
+
+# ---- benchmark-sized layers -------------------------------------------------------------
+@pytest.fixture(scope="module")
+def full3(device):
+    shape = synth.SHAPES["h2048-e256-i512-k8-3bit"]
+    layer, ex = _experts(shape, 1001, device)
+    return shape, layer, ex
+
+
+@pytest.mark.parametrize("T", [1, 4, 8])
+def test_decode_full_3bit(device, full3, T):
+    from kandiga_amd.moe import SparseMoeBlock
+
+    shape, layer, ex = full3
+    x, logits = synth.make_inputs(shape, T, 2000 + T)
+    out, idx, w = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device),
+                                     return_routing=True)
+    ref = O.moe_layer(layer, x, logits, shape.top_k, 3, nthreads=8)
+    assert np.array_equal(to_np(idx), ref["idx"])
+    assert_close(to_np(out), ref["out"], what=f"h2048 3bit decode T={T}")
+
+
+def test_decode_full_3bit_fast_mode(device, full3):
+    """K=4 'fast mode' (engine.py:1132-1147): the same experts, top-4 renormalised."""
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+
+    shape, layer, _ex = full3
+    s4 = shape.with_top_k(4)
+    ex4 = QuantizedExperts.from_stacked(s4, layer, device)
+    for T in (1, 8):
+        x, logits = synth.make_inputs(s4, T, 2100 + T)
+        out = SparseMoeBlock(ex4)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device))
+        ref = O.moe_layer(layer, x, logits, 4, 3, nthreads=8)
+        assert_close(to_np(out), ref["out"], what=f"h2048 3bit K=4 T={T}")
+
+
+@pytest.mark.parametrize("T,sample", [(512, 48), (4096, 24)])
+def test_prefill_full_3bit_zipf(device, full3, T, sample):
+    from kandiga_amd.moe import SparseMoeBlock
+
+    shape, layer, ex = full3
+    x, logits = synth.make_inputs(shape, T, 3000 + T, zipf=True)
+    out, idx, w = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device),
+                                     return_routing=True)
+    ref_idx, ref_w = O.route(logits, shape.top_k)
+    assert np.array_equal(to_np(idx), ref_idx)
+    rows = np.random.default_rng(T).choice(T, sample, replace=False)
+    y = O.switch_mlp(layer, x[rows], ref_idx[rows], 3, nthreads=8)
+    assert_close(to_np(out)[rows], O.combine(y, ref_w[rows]), what=f"h2048 3bit prefill T={T}")
+
+
+def test_decode_full_4bit(device):
+    from kandiga_amd.moe import SparseMoeBlock
+
+    shape = synth.SHAPES["h2048-e256-i512-k8-4bit"]
+    layer, ex = _experts(shape, 1002, device)
+    for T in (1, 8, 64):
+        x, logits = synth.make_inputs(shape, T, 2200 + T)
+        xd, ld = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
+        out = SparseMoeBlock(ex)(xd, ld)
+        out32 = SparseMoeBlock(ex)(xd, ld, out_dtype=torch.float32)
+        ref = O.moe_layer(layer, x, logits, 8, 4, nthreads=8)
+        assert_close(to_np(out), ref["out"], what=f"h2048 4bit T={T}")
+        assert_close(to_np(out32), ref["out"], what=f"h2048 4bit T={T} fp32 out")
+
+
+def test_wide_layer_h4096_e512_k10(device):
+    """H=4096, E=512, I=1024, K=10 generated on the device; oracle on the selected experts."""
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+
+    shape = synth.SHAPES["h4096-e512-i1024-k10-3bit"]
+    layer_t = synth.make_layer_torch(shape, 5001, device)
+    ex = QuantizedExperts.from_stacked(shape, layer_t, device)
+    for T, zipf in ((1, False), (8, False), (300, True)):
+        x, logits = synth.make_inputs(shape, T, 5100 + T, zipf=zipf)
+        out = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device))
+        idx, w = O.route(logits, shape.top_k)
+        rows = np.arange(T) if T <= 8 else np.random.default_rng(T).choice(T, 12, replace=False)
+        uniq, pos = remap(idx[rows])
+        sub = torch_layer_subset(layer_t, uniq)
+        y = O.switch_mlp(sub, x[rows], pos, 3, nthreads=8)
+        assert_close(to_np(out)[rows], O.combine(y, w[rows]), what=f"h4096 e512 T={T}")
