@@ -38,7 +38,10 @@ def parse():
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--layers", type=int, default=8, help="distinct layers in the decode stack")
     p.add_argument("--prefill-steps", type=int, default=20)
-    p.add_argument("--quick", action="store_true", help="decode T=1 only (profiling runs)")
+    p.add_argument("--decode", default="1:8,4:8,8:8,1:4,4:4,8:4",
+                   help="decode cases tokens:top_k, comma separated ('' for none)")
+    p.add_argument("--prefill", default="512,2048,4096", help="prefill token counts ('' for none)")
+    p.add_argument("--modes", default="graph,eager", help="decode launch modes")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     return p.parse_args()
@@ -61,6 +64,7 @@ def main():
     log(f"generating {args.layers} layers of {shape.name} ({shape.expert_bytes * E / 2**20:.0f} MiB each)")
     layers = [synth.make_layer_torch(shape, 7000 + i, dev) for i in range(args.layers)]
     experts = {k: [QuantizedExperts.from_stacked(shape.with_top_k(k), L, dev) for L in layers] for k in (8, 4)}
+    log("layers resident")
     torch.cuda.synchronize()
 
     def bytes_alg(T, k, idx):
@@ -115,19 +119,21 @@ def main():
                     calls=reps * L)
 
     results = {}
-    cases = [(1, 8)] if args.quick else [(1, 8), (4, 8), (8, 8), (1, 4), (4, 4), (8, 4)]
+    cases = [tuple(int(v) for v in c.split(":")) for c in args.decode.split(",") if c]
+    modes = [m for m in args.modes.split(",") if m]
     for T, k in cases:
-        for graph in (True, False):
+        for graph in [m == "graph" for m in modes]:
             r = time_decode(T, k, args.steps, args.warmup, graph)
             key = f"decode_T{T}_K{k}_{'graph' if graph else 'eager'}"
             results[key] = r
             log(f"{key}: {r['us_per_layer']:.2f} us/layer  {r['gbs']:.0f} GB/s  U={r['unique_experts']:.1f}")
 
     prefill = {}
-    if not args.quick:
+    ptoks = [int(v) for v in args.prefill.split(",") if v]
+    if ptoks:
         ex = experts[8][0]
         blk = SparseMoeBlock(ex)
-        for T in (512, 2048, 4096):
+        for T in ptoks:
             x, lg = synth.make_inputs_torch(shape, T, 12000 + T, dev, zipf=True)
             ex.reserve(T)
             for _ in range(3):
@@ -146,7 +152,10 @@ def main():
             log(f"prefill T={T}: {us:.1f} us  {T / (us * 1e-6) / 1e6:.2f} M tok/s  "
                 f"{flops / (us * 1e-6) / 1e12:.1f} TFLOP/s")
 
-    head = results["decode_T1_K8_graph"]
+    head = results.get("decode_T1_K8_graph") or next(iter(results.values()), None)
+    if head is None:
+        print(json.dumps({"metric": METRIC, "detail": prefill}), flush=True)
+        return 0
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(layers[0], shape, args.cpu_seconds)

@@ -1,0 +1,231 @@
+"""Pins of the oracle (CPU): each function is checked against an independent statement of
+what the mathematics fixes -- brute force, closed forms, a float64 library matmul -- chosen
+so that a plausible slip (dropped bias, swapped gate/up, transposed down, wrong code order,
+unstable sort, wrong tie rule) fails one of them.
+"""
+import numpy as np
+import pytest
+
+from kandiga_amd import layout, synth
+from oracle import moe_oracle as O
+
+
+# ---- router ---------------------------------------------------------------------------
+def _route_brute(logits, K):
+    T, E = logits.shape
+    idx = np.zeros((T, K), np.int32)
+    w = np.zeros((T, K), np.float64)
+    for t in range(T):
+        order = sorted(range(E), key=lambda e: (-float(logits[t, e]), e))[:K]
+        idx[t] = order
+        p = np.exp(logits[t].astype(np.float64) - logits[t].astype(np.float64).max())
+        p /= p.sum()                                    # full softmax, then renormalise the K
+        w[t] = p[order] / p[order].sum()
+    return idx, w
+
+
+@pytest.mark.parametrize("E,K", [(8, 2), (16, 4), (40, 8), (256, 8), (512, 10)])
+def test_route_brute_force(E, K):
+    rng = np.random.default_rng(E + K)
+    logits = rng.standard_normal((23, E)).astype(np.float32)
+    logits[3] = 0.5                                     # all equal: lowest indices win
+    logits[4, ::2] = logits[4, 1]                       # many ties
+    idx, w = O.route(logits, K)
+    bidx, bw = _route_brute(logits, K)
+    assert np.array_equal(idx, bidx)
+    np.testing.assert_allclose(w, bw, rtol=1e-6)
+    assert np.array_equal(idx[3], np.arange(K))
+    np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-6)
+
+
+def test_route_weights_closed_form():
+    # w_i / w_j = exp(l_i - l_j) for selected i, j
+    rng = np.random.default_rng(1)
+    logits = (rng.standard_normal((9, 64)) * 3).astype(np.float32)
+    idx, w = O.route(logits, 6)
+    sel = np.take_along_axis(logits, idx, 1).astype(np.float64)
+    np.testing.assert_allclose(w[:, 1:] / w[:, :1], np.exp(sel[:, 1:] - sel[:, :1]), rtol=1e-5)
+    assert (np.diff(sel, axis=1) <= 0).all()
+
+
+def test_route_agrees_with_probability_ranking():
+    """The reference kernel's fp32 probability ranking (moe_block.metal:419-505) agrees with
+    the logit ranking on the seeded inputs; a constructed fp32 probability collision is flagged."""
+    shape = synth.SHAPES["h2048-e256-i512-k8-3bit"]
+    _x, logits = synth.make_inputs(shape, 4096, 77, zipf=True)
+    assert O.route_prob_ties(logits, 8).size == 0
+    a, wa = O.route(logits, 8)
+    b, wb = O.route_by_probs(logits, 8)
+    assert np.array_equal(a, b)
+    np.testing.assert_allclose(wa, wb, rtol=2e-6)
+    # two distinct logits whose fp32 exp(l - max) round to the same value
+    row = np.full((1, 16), -30.0, np.float32)
+    row[0, 0] = 0.0
+    base = np.float32(-1.0)
+    row[0, 5] = base
+    row[0, 2] = np.nextafter(base, np.float32(-2.0))   # smaller logit, lower index
+    eb = np.exp(np.float32(row[0, 5]))
+    ea = np.exp(np.float32(row[0, 2]))
+    if eb == ea:  # collision in fp32 exp on this platform
+        assert O.route_prob_ties(row, 2).size == 1
+        assert O.route(row, 2)[0][0, 1] == 5 and O.route_by_probs(row, 2)[0][0, 1] == 2
+
+
+# ---- permutation ------------------------------------------------------------------------
+@pytest.mark.parametrize("T,K,E", [(1, 8, 256), (7, 3, 5), (300, 8, 16), (64, 10, 512)])
+def test_permute_brute_force(T, K, E):
+    rng = np.random.default_rng(T * K)
+    idx = rng.integers(0, E, size=(T, K)).astype(np.int32)
+    if T > 2:
+        idx[1] = idx[0]                                # repeated rows
+    r = O.permute(idx, E)
+    flat = idx.reshape(-1)
+    brute = sorted(range(T * K), key=lambda f: (flat[f], f))
+    assert np.array_equal(r["perm"], brute)
+    assert np.array_equal(r["s_tok"], np.array(brute) // K)
+    assert np.array_equal(r["s_k"], np.array(brute) % K)
+    assert np.array_equal(r["counts"], np.bincount(flat, minlength=E))
+    assert r["offsets"][0] == 0 and r["offsets"][-1] == T * K
+    assert np.array_equal(np.diff(r["offsets"]), r["counts"])
+    assert np.array_equal(r["unique"], np.unique(flat))
+    assert np.array_equal(flat[r["perm"]][r["group_starts"][:-1]], r["unique"])
+
+
+def test_permute_empty():
+    r = O.permute(np.zeros((0, 4), np.int32), 8)
+    assert r["perm"].size == 0 and r["unique"].size == 0 and r["counts"].sum() == 0
+
+
+# ---- combine ----------------------------------------------------------------------------
+def test_combine_closed_form_and_linearity():
+    rng = np.random.default_rng(2)
+    y = rng.standard_normal((5, 4, 33)).astype(np.float32)
+    w = rng.random((5, 4)).astype(np.float32)
+    out = O.combine(y, w)
+    np.testing.assert_allclose(out, np.einsum("tkh,tk->th", y.astype(np.float64), w), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(O.combine(2 * y, w), 2 * out, rtol=1e-6)
+    one = np.zeros_like(w)
+    one[:, 2] = 1
+    assert np.array_equal(O.combine(y, one), y[:, 2])
+
+
+# ---- fp16 conversion --------------------------------------------------------------------
+def test_c_fp16_conversion_matches_numpy():
+    rng = np.random.default_rng(5)
+    vals = np.concatenate([
+        rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 6, 20000),
+        [0.0, -0.0, 65504.0, 65520.0, 1e6, -1e6, 2 ** -24, 2 ** -25, 3 * 2 ** -26, 2 ** -14, 6.1e-5,
+         1 + 2 ** -11, 1 + 3 * 2 ** -11, np.inf, -np.inf],
+    ]).astype(np.float32)
+    got = O.round_f16(vals)
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+# ---- expert MLP ---------------------------------------------------------------------------
+@pytest.mark.parametrize("bits,scale_dtype", [(3, "f16"), (4, "f16"), (3, "bf16"), (4, "bf16")])
+def test_switch_mlp_matches_f64_library_matmul(bits, scale_dtype):
+    shape = synth.LayerShape(192, 128, 6, 3, bits)
+    layer = synth.make_layer(shape, 13, scale_dtype)
+    x, logits = synth.make_inputs(shape, 4, 14)
+    idx, _ = O.route(logits, 3)
+    y = O.switch_mlp(layer, x, idx, bits, scale_dtype, nthreads=3)
+    for t in range(4):
+        for k in range(3):
+            ref = O.expert_mlp_f64(layer, idx[t, k], x[t], bits, scale_dtype)[0]
+            err = O.compare(y[t, k], ref)
+            assert err["rel_l2"] < 2e-6, (t, k, err)
+
+
+def test_switch_mlp_threads_do_not_change_result():
+    shape = synth.LayerShape(128, 64, 9, 8, 3)
+    layer = synth.make_layer(shape, 15)
+    x, logits = synth.make_inputs(shape, 3, 16)
+    idx, _ = O.route(logits, 8)
+    assert np.array_equal(O.switch_mlp(layer, x, idx, 3, nthreads=1), O.switch_mlp(layer, x, idx, 3, nthreads=8))
+
+
+def _uniform_expert_layer(H, I, bits, cg, cu, cd, s=0.03125, b=-0.0625):
+    """One expert whose gate/up/down codes are constant (cg, cu, cd) with one scale/bias."""
+    def proj(rows, cols, c):
+        codes = np.full((1, rows, cols), c, np.uint8)
+        return (layout.pack_codes(codes, bits), np.full((1, rows, cols // 64), s, np.float16).view(np.uint16),
+                np.full((1, rows, cols // 64), b, np.float16).view(np.uint16))
+    L = {}
+    for name, rows, cols, c in (("gate", I, H, cg), ("up", I, H, cu), ("down", H, I, cd)):
+        L[f"{name}_w"], L[f"{name}_s"], L[f"{name}_b"] = proj(rows, cols, c)
+    return L
+
+
+def test_switch_mlp_closed_form_uniform_weights():
+    """Constant codes: g = wg*sum(x), u = wu*sum(x), act = silu(g)*u for every row,
+    y_h = wd * I * act.  Swapping gate/up or dropping a bias changes the value."""
+    H, I, bits = 128, 64, 3
+    cg, cu, cd, s, b = 5, 6, 7, 0.03125, -0.0625
+    L = _uniform_expert_layer(H, I, bits, cg, cu, cd, s, b)
+    x = np.linspace(-1, 1, H).astype(np.float16)[None, :] + np.float16(0.25)
+    sx = float(x.astype(np.float64).sum())
+    wg, wu, wd = cg * s + b, cu * s + b, cd * s + b
+    g, u = wg * sx, wu * sx
+    act = g / (1 + np.exp(-g)) * u
+    y = O.switch_mlp(L, x, np.zeros((1, 1), np.int32), bits)[0, 0]
+    np.testing.assert_allclose(y, wd * I * act, rtol=1e-5)
+    swapped = u / (1 + np.exp(-u)) * g
+    assert abs(swapped - act) > 1e-2 * abs(act)
+    no_bias = (cg * s * sx) / (1 + np.exp(-cg * s * sx)) * (cu * s * sx) * (cd * s) * I
+    assert abs(no_bias - wd * I * act) > 1e-2 * abs(wd * I * act)
+
+
+def test_switch_mlp_zero_weights():
+    """Codes 2**(b-1) with bias -2**(b-1)*s dequantize to exactly zero."""
+    for bits in (3, 4):
+        mid = 2 ** (bits - 1)
+        L = _uniform_expert_layer(128, 64, bits, mid, mid, mid, s=0.0625, b=-mid * 0.0625)
+        x = np.ones((2, 128), np.float16)
+        y = O.switch_mlp(L, x, np.zeros((2, 1), np.int32), bits)
+        assert np.array_equal(y, np.zeros_like(y))
+
+
+def test_expert_mlp_detects_transposed_down():
+    shape = synth.LayerShape(128, 64, 2, 1, 4)
+    layer = synth.make_layer(shape, 17)
+    x, _ = synth.make_inputs(shape, 1, 18)
+    g, u, d = O.expert_weights_f64(layer, 1, 4, 128, 64)
+    xs = x.astype(np.float64)[0]
+    a = O.silu64(g @ xs) * (u @ xs)
+    good = O.expert_mlp_f64(layer, 1, x, 4)[0]
+    np.testing.assert_allclose(good, d @ a, rtol=1e-12)
+    # code order slip: reversing codes within each packed word gives a different result
+    bad = layer.copy()
+    c = layout.unpack_codes(layer["gate_w"], 4, 128)
+    bad["gate_w"] = layout.pack_codes(c.reshape(2, 64, 16, 8)[..., ::-1].reshape(2, 64, 128), 4)
+    assert O.compare(O.expert_mlp_f64(bad, 1, x, 4)[0], good)["rel_l2"] > 1e-2
+
+
+def test_moe_layer_end_to_end_small():
+    shape = synth.LayerShape(128, 64, 8, 2, 3)
+    layer = synth.make_layer(shape, 19)
+    x, logits = synth.make_inputs(shape, 6, 20)
+    r = O.moe_layer(layer, x, logits, 2, 3)
+    ref = np.zeros((6, 128))
+    for t in range(6):
+        for k in range(2):
+            ref[t] += r["w"][t, k] * O.expert_mlp_f64(layer, r["idx"][t, k], x[t], 3)[0]
+    assert O.compare(r["out"], ref)["rel_l2"] < 2e-6
+
+
+def test_golden_fixture_reproduces():
+    """tests/golden/moe_small.npz was written by tests/golden/make_golden.py from the oracle."""
+    import os
+    from tests.golden.make_golden import CASES, build_case
+
+    data = np.load(os.path.join(os.path.dirname(__file__), "golden", "moe_small.npz"))
+    for name in CASES:
+        case = build_case(name)
+        assert case["layer_sha256"] == str(data[f"{name}.layer_sha256"]), f"{name}: generator drift"
+        assert np.array_equal(case["idx"], data[f"{name}.idx"])
+        assert np.array_equal(case["perm"], data[f"{name}.perm"])
+        np.testing.assert_allclose(case["w"], data[f"{name}.w"], rtol=1e-6)
+        np.testing.assert_allclose(case["y"], data[f"{name}.y"], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(case["out"], data[f"{name}.out"], rtol=1e-5, atol=1e-6)
