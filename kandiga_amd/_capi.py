@@ -29,6 +29,7 @@ SCALE_F16, SCALE_BF16 = 0, 1
 ACT_SWIGLU, ACT_GELU_TANH = 0, 1
 OUT_F16, OUT_F32 = 0, 1
 DEVERR_BAD_EXPERT = 1
+DEVERR_SPIN = 2
 
 
 class KmoeError(RuntimeError):

@@ -280,8 +280,8 @@ int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, 
   uint16_t* yy = static_cast<uint16_t*>(y);
   hipError_t e;
   if (is_decode(tokens, K)) {
-    e = launch_group_small(idx, tokens, K, c.args.E, w.perm, w.ustart, w.unique, w.scalars, s);
-    if (e == hipSuccess) e = launch_decode(c, xx, tokens, w, yy, 0, false, s);
+    DecodeCall d{xx, nullptr, idx, tokens, nullptr, nullptr, nullptr, &w, yy, 0, false};
+    e = launch_decode(c, d, s);
   } else {
     const int mmt = max_mtiles_for(tokens * K, c.args.E);
     e = launch_permute(idx, tokens * K, K, c.args.E, w, mmt, s);
@@ -330,8 +330,8 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
   if (a.sh_gate) e = launch_shared(c, xx, tokens, w, s);
   if (e != hipSuccess) return hip_fail(e, "shared expert launch");
   if (is_decode(tokens, K)) {
-    e = launch_route_group(logits, tokens, a.E, K, w.idx, w.wts, w.perm, w.ustart, w.unique, w.scalars, s);
-    if (e == hipSuccess) e = launch_decode(c, xx, tokens, w, out, out32, true, s);
+    DecodeCall d{xx, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true};
+    e = launch_decode(c, d, s);
   } else {
     const int mmt = max_mtiles_for(tokens * K, a.E);
     e = launch_route(logits, tokens, a.E, K, w.idx, w.wts, s);

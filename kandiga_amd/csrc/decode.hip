@@ -1,21 +1,28 @@
 // Decode path (1..8 tokens): bandwidth-bound dequant GEMVs over the distinct selected experts.
 //
 // Replaces the reference's per-token CPU expert MLP (kandiga/metal/kandiga_cpu_expert.m:
-// 355-401 per expert, :471-552 for the K-way fan-out; kandiga/engine.py:727-735 loops it
-// over tokens).  Every distinct expert selected by any token is read from HBM once per
-// layer and applied to all tokens routed to it.
+// 355-401 per expert, :471-552 for the K-way fan-out; kandiga/engine.py:727-735 loops it over
+// tokens) and the router/combine around it (moe_block.metal:419-539).  Every distinct expert
+// selected by any token is read from HBM once per layer and applied to all tokens routed to it.
 //
-//   dec_gateup_kernel: grid = (distinct-expert slot, block of 4*RW intermediate rows).
-//     x of the expert's tokens is staged in LDS in pair order with per-chunk sums; each
-//     wave streams RW gate rows and the same RW up rows (one 32-code chunk per lane per
-//     step, 12/16-byte loads), accumulates q*x with v_dot2_f32_f16 on raw codes and
-//     applies s*2^24*dot + b*sum(x) per chunk, reduces across the wave and writes
-//     act = silu(gate) * up (fp16, pair order) for every (expert, token) row.
-//   dec_down_kernel: grid = blocks of 64/LPR output rows (LPR lanes per row).  The four
-//     waves split the distinct experts; each lane accumulates w[t,k] * (down row . act)
-//     per token, and the waves' partials are added in a fixed order in LDS, so the
-//     combine (moe_block.metal:515-539) is fused and deterministic.  The per-assignment
-//     variant writes y[t,k,:] instead (the switch_mlp contract, engine.py:670-739).
+// Two launches per layer.  On MI355X a kernel boundary (~1.6 us) is the cheapest grid-wide
+// barrier: measured agent-scope counter or flag barriers cost 6-28 us for 256-512 workgroups.
+//
+//   dec_stage1_kernel: grid = (distinct-expert slot, block of 4*RW intermediate rows).  Every
+//     workgroup stages x of all tokens in LDS (pair order, with per-chunk sums), recomputes
+//     the routing (DPP arg-max per token) or reads the given indices, and groups the T*K
+//     assignments by expert with a stable rank; workgroup 0 publishes routing and grouping.
+//     Each wave then streams RW gate rows and the same RW up rows of its expert (one 32-code
+//     chunk per lane per step), accumulates q*x with v_dot2_f32_f16 on raw codes, applies
+//     s*2^24*dot + b*sum(x) per chunk, reduces across the wave with DPP and writes
+//     act = silu(gate) * up as two fp16 planes (hi, lo: hi + lo carries ~22 bits) in pair
+//     order.  While its loads are in flight it also touches its share of the expert's down
+//     rows, so stage 2 finds them in the memory-side cache.
+//   dec_stage2_kernel: grid = blocks of 64/LPR output rows (LPR lanes per row).  The four
+//     waves split the distinct experts; each lane accumulates w[t,k] * (down row . act) per
+//     token and the waves' partials are added in a fixed order in LDS, so the combine
+//     (moe_block.metal:515-539) is fused and deterministic.  The per-assignment variant writes
+//     y[t,k,:] instead (the switch_mlp contract, engine.py:670-739).
 #include "kmoe_device.h"
 #include "kmoe_internal.h"
 
@@ -45,6 +52,7 @@ __device__ __forceinline__ int pairpos(int e) {
 
 constexpr float TWO24 = 16777216.0f;
 constexpr uint32_t ONE2 = 0x3C003C00u;  // fp16 pair (1, 1)
+constexpr int DEC_RW = 2;               // gate/up row pairs per wave step
 
 template <int ACT>
 __device__ __forceinline__ float activate(float g, float u) {
@@ -67,73 +75,175 @@ __device__ __forceinline__ void load16(const void* p, uint32_t (&v)[16]) {
   }
 }
 
-template <int BITS, bool BF16, int ACT, int NT, int RW>
-__global__ __launch_bounds__(256) void dec_gateup_kernel(const LayerArgs L, const uint16_t* __restrict__ x, int K,
-                                                         const int32_t* __restrict__ perm,
-                                                         const int32_t* __restrict__ ustart,
-                                                         const int32_t* __restrict__ unique,
-                                                         const int32_t* __restrict__ scalars,
-                                                         uint16_t* __restrict__ act, size_t act_plane,
-                                                         int wgs_per_expert) {
-  extern __shared__ uint32_t smem[];
-  const int u = blockIdx.x / wgs_per_expert;
-  const int rb = blockIdx.x - u * wgs_per_expert;
-  if (u >= scalars[0]) return;
-  const int e = unique[u];
-  const int p0 = ustart[u];
-  const int na = min(ustart[u + 1] - p0, NT);
-  const int H = L.H, I = L.I, nch = H / CHUNK;
-  uint32_t* xs = smem;                                               // [NT][nch][16]
-  float* xsum = reinterpret_cast<float*>(smem + (size_t)NT * nch * 16);  // [NT][nch]
-  for (int task = threadIdx.x; task < na * nch; task += blockDim.x) {
-    const int j = task / nch, c = task - j * nch;
-    const int t = perm[p0 + j] / K;
+struct Stage1Args {
+  LayerArgs L;
+  const uint16_t* x;        // [T][H]
+  const float* logits;      // [T][E] (routing mode) or null
+  const int32_t* idx_in;    // [T][K] (given-indices mode) or null
+  int T, K;
+  int32_t* idx_out;         // [T][K] routing (workgroup 0), may be null
+  float* w_out;             // [T][K]
+  int32_t* perm;            // grouping for stage 2 (workgroup 0)
+  int32_t* ustart;
+  int32_t* unique;
+  int32_t* scalars;         // [0] = distinct experts, [2] = device error flags
+  uint16_t* act;            // [2][T*K][I]
+  size_t act_plane;
+  int wgs_per_expert;
+};
+
+template <int BITS, bool BF16, int ACT, int NT, bool ROUTE>
+__global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
+  extern __shared__ uint32_t dyn[];
+  __shared__ int32_t s_e[DEC_MAX_ASSIGN];
+  __shared__ float s_w[DEC_MAX_ASSIGN];
+  __shared__ int32_t s_perm[DEC_MAX_ASSIGN];
+  __shared__ int32_t s_unique[DEC_MAX_ASSIGN];
+  __shared__ int32_t s_ustart[DEC_MAX_ASSIGN + 1];
+  __shared__ int32_t s_tmp[4];
+
+  const LayerArgs& L = A.L;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int T = A.T, K = A.K, TK = T * K;
+  const int H = L.H, I = L.I, E = L.E;
+  const int nch = H / CHUNK;
+  uint32_t* xs = dyn;                                                  // [T][nch][16]
+  float* xsum = reinterpret_cast<float*>(dyn + (size_t)T * nch * 16);  // [T][nch]
+  const bool lead = blockIdx.x == 0;
+
+  // x of every token, pair order, with per-chunk sums.  Each thread's first chunk is loaded
+  // before the routing code so its latency overlaps the logits loads.
+  const int ntask = T * nch;
+  uint32_t xpre[16];
+  if (tid < ntask) load16(A.x + (size_t)(tid / nch) * H + (size_t)(tid % nch) * CHUNK, xpre);
+
+  // routing, or the given indices (out-of-range experts are dropped and flagged)
+  if constexpr (ROUTE) {
+    for (int t = wave; t < T; t += 4) {
+      const float* row = A.logits + (size_t)t * E;
+      int32_t* io = lead && A.idx_out ? A.idx_out + t * K : nullptr;
+      float* wo = lead && A.w_out ? A.w_out + t * K : nullptr;
+      KMOE_TOPK_DISPATCH(E, (wave_topk<EPL_>(row, E, K, io, wo, s_e + t * K, s_w + t * K)));
+    }
+  } else {
+    for (int a = tid; a < TK; a += 256) {
+      const int e = A.idx_in[a];
+      s_e[a] = (e >= 0 && e < E) ? e : -1;
+    }
+  }
+  for (int task = tid; task < ntask; task += 256) {
     uint32_t nat[16], pr[16];
-    load16(x + (size_t)t * H + (size_t)c * CHUNK, nat);
+    if (task == tid) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) nat[q] = xpre[q];
+    } else {
+      load16(A.x + (size_t)(task / nch) * H + (size_t)(task % nch) * CHUNK, nat);
+    }
     to_pair_order<BITS>(nat, pr);
-    uint4* dst = reinterpret_cast<uint4*>(xs + ((size_t)j * nch + c) * 16);
+    uint4* dst = reinterpret_cast<uint4*>(xs + (size_t)task * 16);
 #pragma unroll
     for (int q = 0; q < 4; ++q) dst[q] = make_uint4(pr[4 * q], pr[4 * q + 1], pr[4 * q + 2], pr[4 * q + 3]);
-    float s = 0.f;
+    float sm = 0.f;
 #pragma unroll
-    for (int m = 0; m < 16; ++m) s = fdot2(nat[m], ONE2, s);
-    xsum[j * nch + c] = s;
+    for (int m = 0; m < 16; ++m) sm = fdot2(nat[m], ONE2, sm);
+    xsum[task] = sm;
   }
   __syncthreads();
+  // stable grouping: rank of (expert, assignment) among the valid assignments
+  const int my_e = tid < TK ? s_e[tid] : -1;
+  if (my_e >= 0) {
+    const int key = my_e * DEC_MAX_ASSIGN + tid;
+    int r = 0;
+    for (int b = 0; b < TK; ++b) {
+      const int eb = s_e[b];
+      r += (eb >= 0) & ((eb * DEC_MAX_ASSIGN + b) < key);
+    }
+    s_perm[r] = tid;
+  }
+  int nvalid;
+  block_prefix_count(my_e >= 0, s_tmp, &nvalid);  // its barriers also order the s_perm writes
+  int pe = -1;
+  bool first = false;
+  if (tid < nvalid) {
+    pe = s_e[s_perm[tid]];
+    first = tid == 0 || s_e[s_perm[tid - 1]] != pe;
+  }
+  int nu;
+  const int ur = block_prefix_count(first, s_tmp, &nu);
+  if (first) {
+    s_unique[ur] = pe;
+    s_ustart[ur] = tid;
+  }
+  if (tid == 0) s_ustart[nu] = nvalid;
+  __syncthreads();
+  if (lead) {
+    if (tid < nvalid) A.perm[tid] = s_perm[tid];
+    if (tid < nu) A.unique[tid] = s_unique[tid];
+    if (tid <= nu) A.ustart[tid] = s_ustart[tid];
+    if (tid == 0) {
+      A.scalars[0] = nu;
+      if (nvalid != TK) atomicOr(&A.scalars[2], DEVERR_BAD_EXPERT);
+    }
+  }
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int ib = rb * (4 * RW) + wave * RW;
+  // (expert slot, block of 4*RW rows) items, grid-strided over the workgroups
+  const int nitems = nu * A.wgs_per_expert;
+  uint32_t touch = 0;
+  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+  const int u = item / A.wgs_per_expert;
+  const int rb = item - u * A.wgs_per_expert;
+  const int e = s_unique[u];
+  const int p0 = s_ustart[u];
+  const int na = min(s_ustart[u + 1] - p0, NT);
+
+  // touch this item's share of expert e's down rows (codes, scales, biases)
+  {
+    const size_t dbytes = (size_t)H * I * BITS / 8;
+    const size_t sbytes = (size_t)H * (I / GROUP) * 2;
+    const size_t dshare = ((dbytes + A.wgs_per_expert - 1) / A.wgs_per_expert + 127) & ~(size_t)127;
+    const size_t sshare = ((sbytes + A.wgs_per_expert - 1) / A.wgs_per_expert + 127) & ~(size_t)127;
+    const uint8_t* dw = L.down.w + (size_t)e * L.down.w_stride;
+    const uint8_t* ds = reinterpret_cast<const uint8_t*>(L.down.s + (size_t)e * L.down.s_stride);
+    const uint8_t* db = reinterpret_cast<const uint8_t*>(L.down.b + (size_t)e * L.down.s_stride);
+    const size_t dend = min(dbytes, (size_t)(rb + 1) * dshare);
+    const size_t send = min(sbytes, (size_t)(rb + 1) * sshare);
+    for (size_t off = (size_t)rb * dshare + (size_t)tid * 128; off < dend; off += 256 * 128)
+      touch += *reinterpret_cast<const uint32_t*>(dw + off);
+    for (size_t off = (size_t)rb * sshare + (size_t)tid * 128; off < send; off += 256 * 128)
+      touch += *reinterpret_cast<const uint32_t*>(ds + off) + *reinterpret_cast<const uint32_t*>(db + off);
+  }
+
+  const int ib = rb * (4 * DEC_RW) + wave * DEC_RW;
   const size_t rbytes = (size_t)H * BITS / 8;
   const int ng = H / GROUP;
   const uint8_t* gw = L.gate.w + (size_t)e * L.gate.w_stride + (size_t)ib * rbytes;
   const uint8_t* uw = L.up.w + (size_t)e * L.up.w_stride + (size_t)ib * rbytes;
   const size_t gso = (size_t)e * L.gate.s_stride + (size_t)ib * ng;
   const size_t uso = (size_t)e * L.up.s_stride + (size_t)ib * ng;
-  const uint16_t* gs = L.gate.s + gso;
-  const uint16_t* gb = L.gate.b + gso;
-  const uint16_t* us = L.up.s + uso;
-  const uint16_t* ub = L.up.b + uso;
-
-  float ag[RW][NT], au[RW][NT];
+  int tok[NT];
 #pragma unroll
-  for (int r = 0; r < RW; ++r)
+  for (int j = 0; j < NT; ++j) tok[j] = j < na ? s_perm[p0 + j] / K : 0;
+
+  float ag[DEC_RW][NT], au[DEC_RW][NT];
+#pragma unroll
+  for (int r = 0; r < DEC_RW; ++r)
 #pragma unroll
     for (int j = 0; j < NT; ++j) ag[r][j] = au[r][j] = 0.f;
 
   for (int c = lane; c < nch; c += 64) {
-    uint32_t gd[RW][4], ud[RW][4];
-    uint16_t gsc[RW], gbi[RW], usc[RW], ubi[RW];
+    uint32_t gd[DEC_RW][4], ud[DEC_RW][4];
+    uint16_t gsc[DEC_RW], gbi[DEC_RW], usc[DEC_RW], ubi[DEC_RW];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
+    for (int r = 0; r < DEC_RW; ++r) {
       load_chunk<BITS>(gw + r * rbytes, c, gd[r]);
       load_chunk<BITS>(uw + r * rbytes, c, ud[r]);
-      gsc[r] = gs[r * ng + (c >> 1)];
-      gbi[r] = gb[r * ng + (c >> 1)];
-      usc[r] = us[r * ng + (c >> 1)];
-      ubi[r] = ub[r * ng + (c >> 1)];
+      gsc[r] = L.gate.s[gso + r * ng + (c >> 1)];
+      gbi[r] = L.gate.b[gso + r * ng + (c >> 1)];
+      usc[r] = L.up.s[uso + r * ng + (c >> 1)];
+      ubi[r] = L.up.b[uso + r * ng + (c >> 1)];
     }
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
+    for (int r = 0; r < DEC_RW; ++r) {
       uint32_t cg[16], cu[16];
       unpack_chunk<BITS, false>(gd[r], cg);
       unpack_chunk<BITS, false>(ud[r], cu);
@@ -143,8 +253,8 @@ __global__ __launch_bounds__(256) void dec_gateup_kernel(const LayerArgs L, cons
       for (int j = 0; j < NT; ++j) {
         if (j < na) {
           uint32_t xv[16];
-          load16(xs + ((size_t)j * nch + c) * 16, xv);
-          const float xsm = xsum[j * nch + c];
+          load16(xs + ((size_t)tok[j] * nch + c) * 16, xv);
+          const float xsm = xsum[tok[j] * nch + c];
           ag[r][j] += sg * chunk_dot(cg, xv) + bg * xsm;
           au[r][j] += su * chunk_dot(cu, xv) + bu * xsm;
         }
@@ -152,59 +262,67 @@ __global__ __launch_bounds__(256) void dec_gateup_kernel(const LayerArgs L, cons
     }
   }
 #pragma unroll
-  for (int r = 0; r < RW; ++r) {
+  for (int r = 0; r < DEC_RW; ++r) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       if (j < na) {
-        const float g = wave_sum(ag[r][j]);
-        const float uu = wave_sum(au[r][j]);
+        const float g = wave_sum_dpp(ag[r][j]);
+        const float uu = wave_sum_dpp(au[r][j]);
         if (lane == 0) {
           const int i = ib + r;
           const float a = activate<ACT>(g, uu);
           const _Float16 hi = (_Float16)a;
           const _Float16 lo = (_Float16)(a - (float)hi);
           const size_t o = (size_t)(p0 + j) * I + (i & ~31) + pairpos<BITS>(i & 31);
-          act[o] = __builtin_bit_cast(uint16_t, hi);
-          act[act_plane + o] = __builtin_bit_cast(uint16_t, lo);
+          A.act[o] = __builtin_bit_cast(uint16_t, hi);
+          A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
         }
       }
     }
   }
+  }  // item loop
+  // consume the touched words so the loads are kept (the condition is never true)
+  if (touch == 0x9E3779B9u && blockIdx.x == 0x7FFFFFFF) A.scalars[63] = (int32_t)touch;
 }
 
 template <int BITS, bool BF16, int NT, bool COMBINE>
-__global__ __launch_bounds__(256) void dec_down_kernel(const LayerArgs L, int T, int K,
-                                                       const int32_t* __restrict__ perm,
-                                                       const int32_t* __restrict__ ustart,
-                                                       const int32_t* __restrict__ unique,
-                                                       const int32_t* __restrict__ scalars,
-                                                       const float* __restrict__ wts,
-                                                       const uint16_t* __restrict__ act, size_t act_plane,
-                                                       void* __restrict__ out, int out32,
-                                                       const float* __restrict__ shared_out, int lpr_log2) {
-  extern __shared__ float sm2[];
+__global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int T, int K,
+                                                         const int32_t* __restrict__ perm,
+                                                         const int32_t* __restrict__ ustart,
+                                                         const int32_t* __restrict__ unique,
+                                                         const int32_t* __restrict__ scalars,
+                                                         const float* __restrict__ wts,
+                                                         const uint16_t* __restrict__ act, size_t act_plane,
+                                                         void* __restrict__ out, int out32,
+                                                         const float* __restrict__ shared_out, int lpr_log2) {
+  __shared__ int32_t s_perm[DEC_MAX_ASSIGN];
+  __shared__ int32_t s_unique[DEC_MAX_ASSIGN];
+  __shared__ int32_t s_ustart[DEC_MAX_ASSIGN + 1];
+  __shared__ float s_w[DEC_MAX_ASSIGN];
+  __shared__ float red[4 * 32 * 8];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int H = L.H, I = L.I, nchI = I / CHUNK;
-  const int U = scalars[0];
-  const int npos = ustart[U];
-  const int LPR = 1 << lpr_log2, RPS = 64 >> lpr_log2;
-  float* asum = sm2;                              // [T*K][nchI]
-  float* red = sm2 + (size_t)T * K * nchI;        // [4][RPS][NT]
-  for (int task = threadIdx.x; task < npos * nchI; task += blockDim.x) {
-    const int pos = task / nchI, c = task - pos * nchI;
-    uint32_t v[16], vl[16];
-    load16(act + (size_t)pos * I + (size_t)c * CHUNK, v);
-    load16(act + act_plane + (size_t)pos * I + (size_t)c * CHUNK, vl);
-    float s = 0.f, sl = 0.f;
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      s = fdot2(v[m], ONE2, s);
-      sl = fdot2(vl[m], ONE2, sl);
+  // routing metadata in one round of independent loads (entries past the valid count are unused)
+  const int TK = T * K;
+  __shared__ float s_wa[DEC_MAX_ASSIGN];
+  __shared__ int32_t s_U;
+  if (tid == 0) s_U = scalars[0];
+  const int nuq = min(TK, L.E);  // distinct experts are at most min(T*K, E)
+  for (int q = tid; q <= TK; q += 256) {
+    if (q <= nuq) s_ustart[q] = ustart[q];
+    if (q < nuq) s_unique[q] = unique[q];
+    if (q < TK) {
+      s_perm[q] = perm[q];
+      if (COMBINE) s_wa[q] = wts[q];
     }
-    asum[task] = s + sl;
   }
   __syncthreads();
+  const int U = s_U;
+  const int npos = s_ustart[U];
+  for (int q = tid; q < npos; q += 256) s_w[q] = COMBINE ? s_wa[s_perm[q]] : 0.f;
+  __syncthreads();
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int LPR = 1 << lpr_log2, RPS = 64 >> lpr_log2;
   const int rl = lane >> lpr_log2;
   const int cl = lane & (LPR - 1);
   const int h = blockIdx.x * RPS + rl;
@@ -215,33 +333,37 @@ __global__ __launch_bounds__(256) void dec_down_kernel(const LayerArgs L, int T,
   for (int j = 0; j < NT; ++j) acc[j] = 0.f;
 
   for (int uu = wave; uu < U; uu += 4) {
-    const int e = unique[uu], p0 = ustart[uu];
-    const int na = min(ustart[uu + 1] - p0, NT);
+    const int e = s_unique[uu], p0 = s_ustart[uu];
+    const int na = min(s_ustart[uu + 1] - p0, NT);
     const uint8_t* dw = L.down.w + (size_t)e * L.down.w_stride + (size_t)h * rbytes;
     const size_t dso = (size_t)e * L.down.s_stride + (size_t)h * ng;
-    const uint16_t* ds = L.down.s + dso;
-    const uint16_t* db = L.down.b + dso;
     float accj[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) accj[j] = 0.f;
     for (int c = cl; c < nchI; c += LPR) {
       uint32_t d[4];
       load_chunk<BITS>(dw, c, d);
-      const float sc = scale_to_f32<BF16>(ds[c >> 1]) * TWO24, bi = scale_to_f32<BF16>(db[c >> 1]);
+      const float sc = scale_to_f32<BF16>(L.down.s[dso + (c >> 1)]) * TWO24;
+      const float bi = scale_to_f32<BF16>(L.down.b[dso + (c >> 1)]);
       uint32_t cp[16];
       unpack_chunk<BITS, false>(d, cp);
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         if (j < na) {
           const int pos = p0 + j;
-          uint32_t xv[16], xl[16];
-          load16(act + (size_t)pos * I + (size_t)c * CHUNK, xv);
+          uint32_t xh[16], xl[16];
+          load16(act + (size_t)pos * I + (size_t)c * CHUNK, xh);
           load16(act + act_plane + (size_t)pos * I + (size_t)c * CHUNK, xl);
-          const float part = sc * (chunk_dot(cp, xv) + chunk_dot(cp, xl)) + bi * asum[pos * nchI + c];
+          float sh = 0.f, sl = 0.f;
+#pragma unroll
+          for (int m = 0; m < 16; ++m) {
+            sh = fdot2(xh[m], ONE2, sh);
+            sl = fdot2(xl[m], ONE2, sl);
+          }
+          const float part = sc * (chunk_dot(cp, xh) + chunk_dot(cp, xl)) + bi * (sh + sl);
           if constexpr (COMBINE) {
-            const int a = perm[pos];
-            const int t = a / K;
-            const float wv = wts[a] * part;
+            const int t = s_perm[pos] / K;
+            const float wv = s_w[pos] * part;
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt) acc[tt] += tt == t ? wv : 0.f;
           } else {
@@ -255,7 +377,7 @@ __global__ __launch_bounds__(256) void dec_down_kernel(const LayerArgs L, int T,
       for (int j = 0; j < NT; ++j) {
         if (j < na) {
           const float v = group_sum(accj[j], LPR);
-          if (cl == 0) static_cast<uint16_t*>(out)[(size_t)perm[p0 + j] * H + h] = f32_to_f16_bits(v);
+          if (cl == 0) static_cast<uint16_t*>(out)[(size_t)s_perm[p0 + j] * H + h] = f32_to_f16_bits(v);
         }
       }
     }
@@ -316,13 +438,6 @@ __global__ void dequant_kernel(const QProj P, int in_dim, int expert, int row0, 
 
 // ---- launchers --------------------------------------------------------------------------
 static int nt_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8; }
-constexpr int DEC_RW = 2;
-
-size_t decode_lds_bytes(const LayerConfig& c, int T) {
-  const int nt = nt_for(T);
-  const size_t nch = (size_t)c.args.H / CHUNK;
-  return (size_t)nt * nch * 16 * 4 + (size_t)nt * nch * 4;
-}
 
 static int lpr_log2_for(int I) {
   const int nchI = I / CHUNK;
@@ -331,52 +446,75 @@ static int lpr_log2_for(int I) {
   return l;
 }
 
-template <int BITS, bool BF16, int ACT, int NT>
-static hipError_t decode_impl(const LayerConfig& c, const uint16_t* x, int T, const Work& w, void* out,
-                              int out32, bool combine, hipStream_t s) {
-  const LayerArgs& L = c.args;
-  const int K = c.top_k;
-  const int max_u = min(T * K, L.E);
-  const size_t act_plane = (size_t)T * K * L.I;
-  const int wgs_per_expert = L.I / (4 * DEC_RW);
-  const size_t lds1 = decode_lds_bytes(c, T);
-  if (lds1 > 65536) {
-    hipError_t ae = hipFuncSetAttribute(reinterpret_cast<const void*>(&dec_gateup_kernel<BITS, BF16, ACT, NT, DEC_RW>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+size_t decode_lds_bytes(const LayerConfig& c, int T) {
+  const size_t nch = (size_t)c.args.H / CHUNK;
+  return (size_t)T * nch * 16 * 4 + (size_t)T * nch * 4;
+}
+
+template <typename KERN>
+static hipError_t launch_stage1(KERN k1, int grid, size_t lds, hipStream_t s, const Stage1Args& A) {
+  if (lds > 65536) {
+    hipError_t ae =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(k1), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (ae != hipSuccess) return ae;
   }
-  hipLaunchKernelGGL((dec_gateup_kernel<BITS, BF16, ACT, NT, DEC_RW>), dim3(max_u * wgs_per_expert), dim3(256), lds1,
-                     s, L, x, K, w.perm, w.ustart, w.unique, w.scalars, w.act, act_plane, wgs_per_expert);
-  hipError_t err = hipGetLastError();
+  hipLaunchKernelGGL(k1, dim3(grid), dim3(256), lds, s, A);
+  return hipGetLastError();
+}
+
+template <int BITS, bool BF16, int ACT, int NT>
+static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStream_t s) {
+  const LayerArgs& L = c.args;
+  const int K = c.top_k, T = d.T;
+  const Work& w = *d.w;
+  Stage1Args A;
+  A.L = L;
+  A.x = d.x;
+  A.logits = d.logits;
+  A.idx_in = d.idx_in;
+  A.T = T;
+  A.K = K;
+  A.idx_out = d.idx_out;
+  A.w_out = d.w_out;
+  A.perm = w.perm;
+  A.ustart = w.ustart;
+  A.unique = w.unique;
+  A.scalars = w.scalars;
+  A.act = w.act;
+  A.act_plane = (size_t)T * K * L.I;
+  A.wgs_per_expert = L.I / (4 * DEC_RW);
+  const int grid1 = min(min(T * K, L.E) * A.wgs_per_expert, 1024);
+  const size_t lds1 = decode_lds_bytes(c, T);
+  hipError_t err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, true>, grid1, lds1, s, A)
+                            : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, false>, grid1, lds1, s, A);
   if (err != hipSuccess) return err;
   const int l2 = lpr_log2_for(L.I);
   const int rps = 64 >> l2;
-  const size_t lds2 = ((size_t)T * K * (L.I / CHUNK) + (size_t)4 * rps * NT) * sizeof(float);
-  if (combine) {
-    hipLaunchKernelGGL((dec_down_kernel<BITS, BF16, NT, true>), dim3(L.H / rps), dim3(256), lds2, s, L, T, K, w.perm,
-                       w.ustart, w.unique, w.scalars, w.wts, w.act, act_plane, out, out32,
-                       c.args.sh_gate ? (const float*)w.shared_out : nullptr, l2);
+  if (d.combine) {
+    hipLaunchKernelGGL((dec_stage2_kernel<BITS, BF16, NT, true>), dim3(L.H / rps), dim3(256), 0, s, L, T, K, w.perm,
+                       w.ustart, w.unique, w.scalars, d.wts, w.act, A.act_plane, d.out, d.out32,
+                       L.sh_gate ? (const float*)w.shared_out : nullptr, l2);
   } else {
-    hipLaunchKernelGGL((dec_down_kernel<BITS, BF16, NT, false>), dim3(L.H / rps), dim3(256), lds2, s, L, T, K,
-                       w.perm, w.ustart, w.unique, w.scalars, w.wts, w.act, act_plane, out, 0, (const float*)nullptr, l2);
+    hipLaunchKernelGGL((dec_stage2_kernel<BITS, BF16, NT, false>), dim3(L.H / rps), dim3(256), 0, s, L, T, K, w.perm,
+                       w.ustart, w.unique, w.scalars, d.wts, w.act, A.act_plane, d.out, 0, (const float*)nullptr,
+                       l2);
   }
   return hipGetLastError();
 }
 
 template <int BITS, bool BF16, int ACT>
-static hipError_t decode_nt(const LayerConfig& c, const uint16_t* x, int T, const Work& w, void* out, int out32,
-                            bool comb, hipStream_t s) {
-  switch (nt_for(T)) {
-    case 1: return decode_impl<BITS, BF16, ACT, 1>(c, x, T, w, out, out32, comb, s);
-    case 2: return decode_impl<BITS, BF16, ACT, 2>(c, x, T, w, out, out32, comb, s);
-    case 4: return decode_impl<BITS, BF16, ACT, 4>(c, x, T, w, out, out32, comb, s);
-    default: return decode_impl<BITS, BF16, ACT, 8>(c, x, T, w, out, out32, comb, s);
+static hipError_t decode_nt(const LayerConfig& c, const DecodeCall& d, hipStream_t s) {
+  switch (nt_for(d.T)) {
+    case 1: return decode_impl<BITS, BF16, ACT, 1>(c, d, s);
+    case 2: return decode_impl<BITS, BF16, ACT, 2>(c, d, s);
+    case 4: return decode_impl<BITS, BF16, ACT, 4>(c, d, s);
+    default: return decode_impl<BITS, BF16, ACT, 8>(c, d, s);
   }
 }
 
-hipError_t launch_decode(const LayerConfig& c, const uint16_t* x, int T, const Work& w, void* out, int out32,
-                         bool combine, hipStream_t s) {
-#define KMOE_DEC(B, F, A) decode_nt<B, F, A>(c, x, T, w, out, out32, combine, s)
+hipError_t launch_decode(const LayerConfig& c, const DecodeCall& d, hipStream_t s) {
+  if (d.T < 1 || d.T > DEC_MAX_TOKENS || d.T * c.top_k > DEC_MAX_ASSIGN) return hipErrorInvalidValue;
+#define KMOE_DEC(B, F, A) decode_nt<B, F, A>(c, d, s)
   if (c.bits == 3) {
     if (c.bf16_scales) return c.act ? KMOE_DEC(3, true, 1) : KMOE_DEC(3, true, 0);
     return c.act ? KMOE_DEC(3, false, 1) : KMOE_DEC(3, false, 0);

@@ -199,6 +199,161 @@ __device__ __forceinline__ float group_sum(float v, int width) {
   return v;
 }
 
+// DPP move of a 32-bit value (lanes whose source is masked off receive 0).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<CTRL, ROW_MASK>(__float_as_uint(v)));
+}
+
+// Wave64 sum with DPP: quad_perm [1,0,3,2], [2,3,0,1], row_ror 4, 8 give every lane its row
+// sum; row_bcast 15 (rows 1,3) and row_bcast 31 (rows 2,3) accumulate rows into lane 63.
+// Returns the total in every lane.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x124>(v);
+  v += dpp_f32<0x128>(v);
+  v += dpp_f32<0x142, 0xA>(v);
+  v += dpp_f32<0x143, 0xC>(v);
+  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = dpp_u32<CTRL, ROW_MASK>((uint32_t)v);
+  const uint32_t hi = dpp_u32<CTRL, ROW_MASK>((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Wave64 maximum of unsigned 64-bit values (0 is the identity), same DPP pattern.
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
+  v = max_u64(v, dpp_u64<0xB1>(v));
+  v = max_u64(v, dpp_u64<0x4E>(v));
+  v = max_u64(v, dpp_u64<0x124>(v));
+  v = max_u64(v, dpp_u64<0x128>(v));
+  v = max_u64(v, dpp_u64<0x142, 0xA>(v));
+  v = max_u64(v, dpp_u64<0x143, 0xC>(v));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Orderable key of a router logit: larger logit -> larger key, +0 == -0, NaN below all.
+__device__ __forceinline__ uint32_t logit_key(float v) {
+  if (v != v) return 0u;
+  if (v == 0.0f) v = 0.0f;
+  const uint32_t b = __float_as_uint(v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Top-K of one token's router logits by one wave (moe_block.metal:479-503 semantics): K rounds
+// of a DPP arg-max over the composite key (logit key << 32 | ~index), so equal logits go to the
+// lower index; weights exp(l_k - l_max) / sum_j exp(l_j - l_max), summed in k order.  Each lane
+// holds EPL logits (EPL * 64 >= E) and keeps the best of its remaining keys, so a round is one
+// wave max plus a rescan in the lane that supplied the winner.
+// Lanes k < K write idx_out[k] / w_out[k] (either may be null) and sel[k] / selw[k] (may be null).
+template <int EPL>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int K, int32_t* idx_out,
+                                          float* w_out, int32_t* sel, float* selw) {
+  const int lane = threadIdx.x & 63;
+  float lv[EPL];
+#pragma unroll
+  for (int m = 0; m < EPL; ++m) {
+    const int e = lane + 64 * m;
+    lv[m] = e < E ? row[e] : 0.0f;
+  }
+  uint64_t keys[EPL];
+  uint64_t best = 0;
+#pragma unroll
+  for (int m = 0; m < EPL; ++m) {
+    const int e = lane + 64 * m;
+    keys[m] = e < E ? (((uint64_t)logit_key(lv[m]) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e)) : 0ull;
+    best = max_u64(best, keys[m]);
+  }
+  int my = 0;
+  float my_l = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const uint64_t wb = wave_max_u64_dpp(best);
+    const int e = (int)(0xFFFFFFFFu - (uint32_t)wb);
+    float tv = 0.0f;
+    if (best == wb) {  // only the lane holding the winner: drop it, keep its logit, rescan
+      uint64_t nb = 0;
+#pragma unroll
+      for (int m = 0; m < EPL; ++m) {
+        if (keys[m] == wb) {
+          tv = lv[m];
+          keys[m] = 0ull;
+        }
+        nb = max_u64(nb, keys[m]);
+      }
+      best = nb;
+    }
+    const float lk = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(tv), e & 63));
+    if (lane == k) {
+      my = e;
+      my_l = lk;
+    }
+  }
+  const float l0 = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(my_l)));
+  const float ex = lane < K ? expf(my_l - l0) : 0.0f;
+  float sum = 0.0f;
+  for (int k = 0; k < K; ++k)
+    sum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(ex), k));
+  if (lane < K) {
+    const float w = ex / sum;
+    if (idx_out) idx_out[lane] = my;
+    if (w_out) w_out[lane] = w;
+    if (sel) sel[lane] = my;
+    if (selw) selw[lane] = w;
+  }
+}
+
+// Runtime E -> EPL dispatch helper for callers.
+#define KMOE_TOPK_DISPATCH(E, CALL)      \
+  do {                                   \
+    if ((E) <= 64) {                     \
+      constexpr int EPL_ = 1;            \
+      CALL;                              \
+    } else if ((E) <= 128) {             \
+      constexpr int EPL_ = 2;            \
+      CALL;                              \
+    } else if ((E) <= 256) {             \
+      constexpr int EPL_ = 4;            \
+      CALL;                              \
+    } else if ((E) <= 512) {             \
+      constexpr int EPL_ = 8;            \
+      CALL;                              \
+    } else {                             \
+      constexpr int EPL_ = 16;           \
+      CALL;                              \
+    }                                    \
+  } while (0)
+
+// Exclusive prefix count of `flag` over the threads of a 256-thread block, plus the total.
+// Uses ballots and a 4-entry LDS array `tmp`; every thread must call it.
+__device__ __forceinline__ int block_prefix_count(bool flag, int32_t* tmp, int* total) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint64_t m = __ballot(flag);
+  if (lane == 0) tmp[wave] = __popcll(m);
+  __syncthreads();
+  int before = __popcll(m & ((1ull << lane) - 1ull));
+  int tot = 0;
+  for (int w = 0; w < 4; ++w) {
+    const int c = tmp[w];
+    before += w < wave ? c : 0;
+    tot += c;
+  }
+  __syncthreads();
+  *total = tot;
+  return before;
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
 __device__ __forceinline__ float gelu_tanh_f32(float g) {

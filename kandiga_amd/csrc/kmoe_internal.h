@@ -43,7 +43,7 @@ struct Work {
   int32_t* offsets;    // [E+1]
   int32_t* unique;     // [E]
   int32_t* ustart;     // [E+1]   group starts of the unique experts
-  int32_t* scalars;    // [0]=num_unique [1]=num GEMM m-tiles [2]=device error flags
+  int32_t* scalars;    // [0]=num_unique [1]=num GEMM m-tiles [2]=device error flags [4,5]=decode sync
   int32_t* mt_expert;  // [max_mtiles]
   int32_t* mt_row0;    // [max_mtiles]
   int32_t* mt_rows;    // [max_mtiles]
@@ -60,17 +60,27 @@ constexpr int DEC_MAX_ASSIGN = 256;
 
 // Device error flag bits (Work::scalars[2]).
 constexpr int DEVERR_BAD_EXPERT = 1;
+constexpr int DEVERR_SPIN = 2;  // a grid-wide wait reached its spin bound
+
+// One decode-path call (1..DEC_MAX_TOKENS tokens): routing from logits, or given indices.
+struct DecodeCall {
+  const uint16_t* x;       // [T][H]
+  const float* logits;     // [T][E], or null when idx_in is given
+  const int32_t* idx_in;   // [T][K], or null when routing
+  int T;
+  int32_t* idx_out;        // routing outputs written by stage 1 (routing mode)
+  float* w_out;
+  const float* wts;        // combine weights read by stage 2 (= w_out in routing mode)
+  const Work* w;
+  void* out;               // combined [T][H] (combine) or per-assignment y [T*K][H] fp16
+  int out32;
+  bool combine;
+};
 
 // ---- launchers (return hipError_t of the launch) ----------------------------------------
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s);
-hipError_t launch_route_group(const float* logits, int T, int E, int K, int32_t* idx, float* wts,
-                              int32_t* perm, int32_t* ustart, int32_t* unique, int32_t* scalars, hipStream_t s);
-hipError_t launch_group_small(const int32_t* idx, int T, int K, int E, int32_t* perm, int32_t* ustart,
-                              int32_t* unique, int32_t* scalars, hipStream_t s);
 hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, hipStream_t s);
-
-hipError_t launch_decode(const LayerConfig& c, const uint16_t* x, int T, const Work& w, void* out, int out32,
-                         bool combine, hipStream_t s);
+hipError_t launch_decode(const LayerConfig& c, const DecodeCall& d, hipStream_t s);
 hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Work& w, int max_mtiles,
                        uint16_t* y16, hipStream_t s);
 hipError_t launch_combine(const float* y32, const float* wts, int T, int K, int H, const float* shared,

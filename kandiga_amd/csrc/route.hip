@@ -18,140 +18,15 @@
 
 namespace kmoe {
 
-// Orderable key of a logit: larger logit -> larger key; +0 and -0 equal; NaN below all.
-__device__ __forceinline__ uint32_t logit_key(float v) {
-  if (v != v) return 0u;
-  if (v == 0.0f) v = 0.0f;
-  const uint32_t b = __float_as_uint(v);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, off, 64);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
-// One wave: top-K of one logits row.  Composite key (logit key << 32 | ~index) makes the
-// maximum unique and puts the lower index first among equal logits.
-template <int EPL>
-__device__ void wave_topk(const float* __restrict__ row, int E, int K, int32_t* __restrict__ idx_out,
-                          float* __restrict__ w_out, int32_t* __restrict__ sel_lds) {
-  const int lane = threadIdx.x & 63;
-  uint64_t keys[EPL];
-#pragma unroll
-  for (int m = 0; m < EPL; ++m) {
-    const int e = lane + 64 * m;
-    keys[m] = e < E ? (((uint64_t)logit_key(row[e]) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e)) : 0ull;
-  }
-  int my_sel = 0;
-  for (int k = 0; k < K; ++k) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int m = 0; m < EPL; ++m) best = keys[m] > best ? keys[m] : best;
-    const uint64_t wb = wave_max_u64(best);
-#pragma unroll
-    for (int m = 0; m < EPL; ++m) keys[m] = keys[m] == wb ? 0ull : keys[m];
-    const int e = (int)(0xFFFFFFFFu - (uint32_t)wb);
-    if (lane == k) my_sel = e;
-  }
-  // weights: lane k < K owns selection k
-  const float l0 = row[__shfl(my_sel, 0, 64)];
-  float ex = 0.0f;
-  if (lane < K) ex = expf(row[my_sel] - l0);
-  float sum = 0.0f;
-  for (int k = 0; k < K; ++k) sum += __shfl(ex, k, 64);  // k order, as the reference sums
-  if (lane < K) {
-    idx_out[lane] = my_sel;
-    w_out[lane] = ex / sum;
-    if (sel_lds) sel_lds[lane] = my_sel;
-  }
-}
-
-template <int EPL>
+template <int UNUSED = 0>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int T, int E, int K,
                                                     int32_t* __restrict__ idx, float* __restrict__ wts) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  wave_topk<EPL>(logits + (size_t)t * E, E, K, idx + (size_t)t * K, wts + (size_t)t * K, nullptr);
-}
-
-// Stable grouping of up to DEC_MAX_ASSIGN assignments whose experts are in LDS (one block).
-__device__ void group_assignments(const int32_t* __restrict__ sh_e, int TK, int E, int32_t* __restrict__ sh_first,
-                                  int32_t* __restrict__ perm, int32_t* __restrict__ ustart,
-                                  int32_t* __restrict__ unique, int32_t* __restrict__ scalars) {
-  for (int a = threadIdx.x; a < TK; a += blockDim.x) {
-    const int e = sh_e[a];
-    int before_same = 0;
-    for (int b = 0; b < a; ++b) before_same += sh_e[b] == e;
-    sh_first[a] = before_same == 0 && e >= 0;
-  }
-  __syncthreads();
-  int nu_local = 0;
-  for (int a = threadIdx.x; a < TK; a += blockDim.x) {
-    const int e = sh_e[a];
-    if (e < 0) continue;  // invalid expert index: dropped, flagged by the caller
-    int less = 0, before_same = 0, uniq_less = 0;
-    for (int b = 0; b < TK; ++b) {
-      const int eb = sh_e[b];
-      less += (eb >= 0) & (eb < e);
-      before_same += (b < a) & (eb == e);
-      uniq_less += sh_first[b] & (eb >= 0) & (eb < e);
-    }
-    perm[less + before_same] = a;
-    if (sh_first[a]) {
-      unique[uniq_less] = e;
-      ustart[uniq_less] = less;
-      nu_local++;
-    }
-  }
-  // number of valid assignments closes the last group
-  __shared__ int s_nu, s_valid;
-  if (threadIdx.x == 0) { s_nu = 0; s_valid = 0; }
-  __syncthreads();
-  if (nu_local) atomicAdd(&s_nu, nu_local);
-  int v = 0;
-  for (int a = threadIdx.x; a < TK; a += blockDim.x) v += sh_e[a] >= 0;
-  if (v) atomicAdd(&s_valid, v);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    scalars[0] = s_nu;
-    ustart[s_nu] = s_valid;
-    if (s_valid != TK) atomicOr(&scalars[2], DEVERR_BAD_EXPERT);
-  }
-}
-
-template <int EPL>
-__global__ __launch_bounds__(256) void route_group_kernel(const float* __restrict__ logits, int T, int E, int K,
-                                                          int32_t* __restrict__ idx, float* __restrict__ wts,
-                                                          int32_t* __restrict__ perm, int32_t* __restrict__ ustart,
-                                                          int32_t* __restrict__ unique,
-                                                          int32_t* __restrict__ scalars) {
-  __shared__ int32_t sh_e[DEC_MAX_ASSIGN];
-  __shared__ int32_t sh_first[DEC_MAX_ASSIGN];
-  for (int t = threadIdx.x >> 6; t < T; t += 4)
-    wave_topk<EPL>(logits + (size_t)t * E, E, K, idx + (size_t)t * K, wts + (size_t)t * K, sh_e + t * K);
-  __syncthreads();
-  group_assignments(sh_e, T * K, E, sh_first, perm, ustart, unique, scalars);
-}
-
-__global__ __launch_bounds__(256) void group_small_kernel(const int32_t* __restrict__ idx, int TK, int E,
-                                                          int32_t* __restrict__ perm, int32_t* __restrict__ ustart,
-                                                          int32_t* __restrict__ unique,
-                                                          int32_t* __restrict__ scalars) {
-  __shared__ int32_t sh_e[DEC_MAX_ASSIGN];
-  __shared__ int32_t sh_first[DEC_MAX_ASSIGN];
-  for (int a = threadIdx.x; a < TK; a += blockDim.x) {
-    const int e = idx[a];
-    sh_e[a] = (e >= 0 && e < E) ? e : -1;
-  }
-  __syncthreads();
-  group_assignments(sh_e, TK, E, sh_first, perm, ustart, unique, scalars);
+  const float* row = logits + (size_t)t * E;
+  int32_t* io = idx + (size_t)t * K;
+  float* wo = wts + (size_t)t * K;
+  KMOE_TOPK_DISPATCH(E, (wave_topk<EPL_>(row, E, K, io, wo, nullptr, nullptr)));
 }
 
 // ---- multi-tile permutation ---------------------------------------------------------------
@@ -299,47 +174,9 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(
 }
 
 // ---- launchers --------------------------------------------------------------------------
-static int epl_for(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16; }
-
-template <int EPL>
-static void route_launch(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s) {
-  hipLaunchKernelGGL(route_kernel<EPL>, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, idx, wts);
-}
-
-template <int EPL>
-static void route_group_launch(const float* logits, int T, int E, int K, int32_t* idx, float* wts, int32_t* perm,
-                               int32_t* ustart, int32_t* unique, int32_t* scalars, hipStream_t s) {
-  hipLaunchKernelGGL(route_group_kernel<EPL>, dim3(1), dim3(256), 0, s, logits, T, E, K, idx, wts, perm, ustart,
-                     unique, scalars);
-}
-
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s) {
   if (T == 0) return hipSuccess;
-  switch (epl_for(E)) {
-    case 1: route_launch<1>(logits, T, E, K, idx, wts, s); break;
-    case 2: route_launch<2>(logits, T, E, K, idx, wts, s); break;
-    case 4: route_launch<4>(logits, T, E, K, idx, wts, s); break;
-    case 8: route_launch<8>(logits, T, E, K, idx, wts, s); break;
-    default: route_launch<16>(logits, T, E, K, idx, wts, s); break;
-  }
-  return hipGetLastError();
-}
-
-hipError_t launch_route_group(const float* logits, int T, int E, int K, int32_t* idx, float* wts, int32_t* perm,
-                              int32_t* ustart, int32_t* unique, int32_t* scalars, hipStream_t s) {
-  switch (epl_for(E)) {
-    case 1: route_group_launch<1>(logits, T, E, K, idx, wts, perm, ustart, unique, scalars, s); break;
-    case 2: route_group_launch<2>(logits, T, E, K, idx, wts, perm, ustart, unique, scalars, s); break;
-    case 4: route_group_launch<4>(logits, T, E, K, idx, wts, perm, ustart, unique, scalars, s); break;
-    case 8: route_group_launch<8>(logits, T, E, K, idx, wts, perm, ustart, unique, scalars, s); break;
-    default: route_group_launch<16>(logits, T, E, K, idx, wts, perm, ustart, unique, scalars, s); break;
-  }
-  return hipGetLastError();
-}
-
-hipError_t launch_group_small(const int32_t* idx, int T, int K, int E, int32_t* perm, int32_t* ustart,
-                              int32_t* unique, int32_t* scalars, hipStream_t s) {
-  hipLaunchKernelGGL(group_small_kernel, dim3(1), dim3(256), 0, s, idx, T * K, E, perm, ustart, unique, scalars);
+  hipLaunchKernelGGL(route_kernel<0>, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, idx, wts);
   return hipGetLastError();
 }
 

@@ -231,3 +231,53 @@ def test_wide_layer_h4096_e512_k10(device):
         sub = torch_layer_subset(layer_t, uniq)
         y = O.switch_mlp(sub, x[rows], pos, 3, nthreads=8)
         assert_close(to_np(out)[rows], O.combine(y, w[rows]), what=f"h4096 e512 T={T}")
+
+
+def test_decode_graph_replays_match_eager(device):
+    """Several replays of a captured stack of decode layers, with eager work between them,
+    each bit-identical to the eager result (the fused kernel resets its own counters)."""
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+
+    shape = synth.LayerShape(512, 256, 32, 8, 3)
+    blocks, ins = [], []
+    for i in range(3):
+        layer = synth.make_layer(shape, 600 + i)
+        ex = QuantizedExperts.from_stacked(shape, layer, device)
+        ex.reserve(4)
+        blocks.append(SparseMoeBlock(ex))
+        x, lg = synth.make_inputs(shape, 1 + i, 700 + i)
+        ins.append((torch.from_numpy(x).to(device), torch.from_numpy(lg).to(device)))
+    eager = [b(*a).clone() for b, a in zip(blocks, ins)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for b, a in zip(blocks, ins):
+            b(*a)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    outs = [None] * 3
+    with torch.cuda.graph(g):
+        for i, (b, a) in enumerate(zip(blocks, ins)):
+            outs[i] = b(*a)
+    for rep in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(3):
+            assert torch.equal(outs[i], eager[i]), f"replay {rep} layer {i}"
+        _ = [b(*a) for b, a in zip(blocks, ins)]   # eager work between replays
+        torch.cuda.synchronize()
+    for b in blocks:
+        assert b.experts.device_status() == 0
+
+
+def test_decode_repeated_calls_deterministic(device, full3):
+    from kandiga_amd.moe import SparseMoeBlock
+
+    shape, layer, ex = full3
+    x, logits = synth.make_inputs(shape, 3, 4242)
+    xd, ld = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
+    blk = SparseMoeBlock(ex)
+    first = blk(xd, ld).clone()
+    for _ in range(20):
+        assert torch.equal(blk(xd, ld), first)
+    assert ex.device_status() == 0
