@@ -2,22 +2,32 @@
 """Benchmark of the routed-expert MoE layer on one MI355X.
 
 Workload of the reported value: decode of one token through a 3-bit top-8 MoE layer
-(hidden 2048, 256 experts, intermediate 512, group 64, fp16 scale/bias), over a stack of
-distinct seeded layers (>= 2.8 GB of expert weights, well beyond the 256 MB MALL) run
-back to back; a step is one layer call.  Reported beside it: decode at 4 and 8 tokens,
-the top-4 "fast mode", and 3-bit prefill of 512/2048/4096 Zipf-routed tokens.
+(hidden 2048, 256 experts, intermediate 512, group 64, fp16 scale/bias), over a stack of 8
+distinct seeded layers (2.8 GB of expert weights resident).  Each layer is called with P
+different token inputs in turn, so one replay of the captured call sequence touches more than
+1 GiB of distinct expert bytes (over 4x the 256 MB memory-side cache) and the bytes come from
+HBM.  A step is one layer call.  Reported beside it: decode at 4 and 8 tokens, the top-4
+"fast mode", and 3-bit prefill of 512/2048/4096 Zipf-routed tokens.
 
 `value` = achieved algorithmic HBM bandwidth of the layer at 1 token, in GB/s:
 bytes_alg = U*expert_bytes + T*H*2 (x) + T*E*4 (logits) + T*H*2 (out) + T*K*8 (routing),
-U = distinct experts selected, divided by the measured time per layer.
+U = distinct experts selected, divided by the measured time per layer call.
 
-The CPU baseline is the oracle's C restatement of the reference expert MLP (K experts of a
-token fanned out over threads, as the reference does) timed on this host.
+`roofline` is that of the dominant kernel (the decode stage 1: routing, gate/up GEMVs and
+SwiGLU), timed with HIP events around each of its launches (kmoe_profile_begin/end) in an
+eager pass over the same calls; its algorithmic bytes per launch are
+U*(gate+up bytes of one expert) + T*H*2 + T*E*4 + T*K*I*4 (act written) + T*K*8.
+`traffic` comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under
+profiles/ for that kernel and workload (null when absent).
+
+The CPU baseline is the oracle's C restatement of the reference expert MLP (the K experts of
+a token fanned out over threads, as the reference does) timed on this host.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -25,6 +35,9 @@ import time
 METRIC = "MoE-layer decode µs/token + HBM GB/s; prefill tokens/s (3-bit, top-8)"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+ROTATE_BYTES = 1.1 * 2 ** 30   # distinct expert bytes touched per replay of the decode sequence
+HERE = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "dec_stage1_kernel_decode_t1_k8_traffic.json")
 
 
 def log(msg: str) -> None:
@@ -34,7 +47,7 @@ def log(msg: str) -> None:
 def parse():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=800, help="timed layer calls (decode)")
+    p.add_argument("--steps", type=int, default=800, help="timed layer calls per decode case")
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--layers", type=int, default=8, help="distinct layers in the decode stack")
     p.add_argument("--prefill-steps", type=int, default=20)
@@ -56,57 +69,66 @@ def main():
     import torch
 
     from kandiga_amd import synth
-    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock, profile_kernels
 
     dev = torch.device("cuda:0")
     shape = synth.SHAPES["h2048-e256-i512-k8-3bit"]
-    H, E, K = shape.hidden, shape.num_experts, shape.top_k
+    H, E, I = shape.hidden, shape.num_experts, shape.intermediate
+    gu_bytes = 2 * I * H * 3 // 8 + 4 * I * (H // 64) * 2   # gate + up codes, scales, biases
     log(f"generating {args.layers} layers of {shape.name} ({shape.expert_bytes * E / 2**20:.0f} MiB each)")
     layers = [synth.make_layer_torch(shape, 7000 + i, dev) for i in range(args.layers)]
     experts = {k: [QuantizedExperts.from_stacked(shape.with_top_k(k), L, dev) for L in layers] for k in (8, 4)}
-    log("layers resident")
+    del layers
     torch.cuda.synchronize()
+    log("layers resident")
+    copy_gbs = measured_copy_gbs(torch, dev)
+    log(f"device copy: {copy_gbs:.0f} GB/s (read + write)")
 
-    def bytes_alg(T, k, idx):
-        U = int(torch.unique(idx).numel())
-        return U * shape.expert_bytes + T * H * 2 + T * E * 4 + T * H * 2 + T * k * 8, U
-
-    def time_decode(T, k, steps, warmup, graph):
+    def decode_case(T, k, graph):
         blocks = [SparseMoeBlock(ex) for ex in experts[k]]
         for ex in experts[k]:
             ex.reserve(T)
-        ins = [synth.make_inputs_torch(shape, T, 9000 + 31 * i + T, dev) for i in range(len(blocks))]
-        outs = [None] * len(blocks)
-        ba, us_ = 0.0, 0.0
-        for i, (b, (x, lg)) in enumerate(zip(blocks, ins)):
-            _o, idx, _w = b(x, lg, return_routing=True)
-            bb, U = bytes_alg(T, k, idx)
-            ba += bb
-            us_ += U
-        ba /= len(blocks)
-        us_ /= len(blocks)
         L = len(blocks)
-        reps = max(1, steps // L)
+        est = min(T * k, E) * shape.expert_bytes
+        P = max(2, math.ceil(ROTATE_BYTES / (L * est)))
+        seq = []  # (block, x, logits) in call order: every layer with input set 0, then set 1, ...
+        for p in range(P):
+            for li, b in enumerate(blocks):
+                x, lg = synth.make_inputs_torch(shape, T, 9000 + 997 * p + 31 * li + T, dev)
+                seq.append((li, b, x, lg))
+        b_alg, b_s1, uniq, seen = [], [], [], [set() for _ in blocks]
+        for li, b, x, lg in seq:
+            _o, idx, _w = b(x, lg, return_routing=True)
+            ids = torch.unique(idx).tolist()
+            U = len(ids)
+            seen[li].update(ids)
+            uniq.append(U)
+            b_alg.append(U * shape.expert_bytes + T * H * 2 + T * E * 4 + T * H * 2 + T * k * 8)
+            b_s1.append(U * gu_bytes + T * H * 2 + T * E * 4 + T * k * I * 4 + T * k * 8)
+        distinct = sum(len(s) for s in seen) * shape.expert_bytes
+        outs = [None] * len(seq)
         if graph:
             g = torch.cuda.CUDAGraph()
             s = torch.cuda.Stream()
             s.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(s):
-                for i, b in enumerate(blocks):
-                    outs[i] = b(*ins[i])
+                for i, (_li, b, x, lg) in enumerate(seq):
+                    outs[i] = b(x, lg)
             torch.cuda.current_stream().wait_stream(s)
             with torch.cuda.graph(g):
-                for i, b in enumerate(blocks):
-                    outs[i] = b(*ins[i])
+                for i, (_li, b, x, lg) in enumerate(seq):
+                    outs[i] = b(x, lg)
 
             def run():
                 g.replay()
         else:
             def run():
-                for i, b in enumerate(blocks):
-                    outs[i] = b(*ins[i])
-        for _ in range(max(1, warmup // L)):
+                for i, (_li, b, x, lg) in enumerate(seq):
+                    outs[i] = b(x, lg)
+        n = len(seq)
+        for _ in range(max(1, math.ceil(args.warmup / n))):
             run()
+        reps = max(1, args.steps // n)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -114,19 +136,37 @@ def main():
             run()
         e1.record()
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * L)
-        return dict(T=T, k=k, us_per_layer=us, gbs=ba / (us * 1e-6) / 1e9, bytes_alg=ba, unique_experts=us_,
-                    calls=reps * L)
+        us = e0.elapsed_time(e1) * 1e3 / (reps * n)
+        ba = sum(b_alg) / n
+        r = dict(T=T, k=k, us_per_layer=us, gbs=ba / (us * 1e-6) / 1e9, bytes_alg=ba,
+                 unique_experts=sum(uniq) / n, calls=reps * n, inputs_per_layer=P,
+                 distinct_expert_bytes_per_replay=distinct)
+        if graph:
+            # per-kernel event timing over one eager pass of the same calls
+            with profile_kernels(4 * n + 16) as prof:
+                for _li, b, x, lg in seq:
+                    b(x, lg)
+            s1 = prof.result.get("dec_stage1_kernel")
+            s2 = prof.result.get("dec_stage2_kernel")
+            if s1 and s2:
+                r["stage1_us"] = s1["mean_ms"] * 1e3
+                r["stage2_us"] = s2["mean_ms"] * 1e3
+                r["stage1_bytes_alg"] = sum(b_s1) / n
+                r["stage1_gbs"] = r["stage1_bytes_alg"] / (s1["mean_ms"] * 1e-3) / 1e9
+        return r
 
     results = {}
     cases = [tuple(int(v) for v in c.split(":")) for c in args.decode.split(",") if c]
     modes = [m for m in args.modes.split(",") if m]
     for T, k in cases:
         for graph in [m == "graph" for m in modes]:
-            r = time_decode(T, k, args.steps, args.warmup, graph)
+            r = decode_case(T, k, graph)
             key = f"decode_T{T}_K{k}_{'graph' if graph else 'eager'}"
             results[key] = r
-            log(f"{key}: {r['us_per_layer']:.2f} us/layer  {r['gbs']:.0f} GB/s  U={r['unique_experts']:.1f}")
+            extra = (f"  stage1 {r['stage1_us']:.2f} us ({r['stage1_gbs']:.0f} GB/s) stage2 {r['stage2_us']:.2f} us"
+                     if "stage1_us" in r else "")
+            log(f"{key}: {r['us_per_layer']:.2f} us/layer  {r['gbs']:.0f} GB/s  U={r['unique_experts']:.1f} "
+                f"P={r['inputs_per_layer']} distinct={r['distinct_expert_bytes_per_replay'] / 2**30:.2f} GiB{extra}")
 
     prefill = {}
     ptoks = [int(v) for v in args.prefill.split(",") if v]
@@ -146,11 +186,18 @@ def main():
             e1.record()
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / args.prefill_steps
-            flops = 2.0 * T * K * 3 * H * shape.intermediate
-            prefill[f"prefill_T{T}"] = dict(T=T, us=us, tokens_per_s=T / (us * 1e-6), tflops=flops / (us * 1e-6) / 1e12,
-                                            mfma_frac=flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS)
+            with profile_kernels(64) as prof:
+                for _ in range(3):
+                    blk(x, lg)
+            kern = {n: round(v["mean_ms"] * 1e3, 2) for n, v in prof.result.items()}
+            flops = 2.0 * T * shape.top_k * 3 * H * I
+            gemm_us = kern.get("gemm_gateup_kernel", 0) + kern.get("gemm_down_kernel", 0)
+            prefill[f"prefill_T{T}"] = dict(
+                T=T, us=us, tokens_per_s=T / (us * 1e-6), tflops=flops / (us * 1e-6) / 1e12,
+                mfma_frac=flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, kernel_us=kern,
+                gemm_mfma_frac=(flops / (gemm_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS) if gemm_us else None)
             log(f"prefill T={T}: {us:.1f} us  {T / (us * 1e-6) / 1e6:.2f} M tok/s  "
-                f"{flops / (us * 1e-6) / 1e12:.1f} TFLOP/s")
+                f"{flops / (us * 1e-6) / 1e12:.1f} TFLOP/s  kernels(us) {kern}")
 
     head = results.get("decode_T1_K8_graph") or next(iter(results.values()), None)
     if head is None:
@@ -158,7 +205,15 @@ def main():
         return 0
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(layers[0], shape, args.cpu_seconds)
+        cpu = cpu_baseline(experts[8][0], shape, args.cpu_seconds)
+
+    roof = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None, "traffic": None}
+    if "stage1_us" in head:
+        roof.update(achieved=round(head["stage1_gbs"], 1), frac=round(head["stage1_gbs"] / HBM_PEAK_GBS, 4),
+                    kernel="dec_stage1_kernel", mean_launch_us=round(head["stage1_us"], 3),
+                    bytes_alg_per_launch=round(head["stage1_bytes_alg"]),
+                    frac_of_measured_copy=round(head["stage1_gbs"] / copy_gbs, 4))
+        roof["traffic"] = stage1_traffic(head["stage1_bytes_alg"])
 
     line = {
         "metric": METRIC,
@@ -171,18 +226,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u3 codes, fp16 activations, fp32 accumulate",
-        "data": "synthetic (seeded MLX-layout 3-bit experts, fp16 scale/bias; random-init)",
+        "dtype": "u3",
+        "data": "synthetic (seeded MLX-layout 3-bit experts, fp16 scale/bias, fp16 activations; random-init)",
         "config": {"workload": "moe-layer decode, 1 token, 3-bit top-8, hidden 2048, 256 experts, "
-                               "intermediate 512, group 64; stack of %d distinct layers" % args.layers,
-                   "tokens": 1, "top_k": K, "hidden": H, "experts": E, "intermediate": shape.intermediate,
+                               "intermediate 512, group 64; stack of %d distinct layers, %d inputs per layer"
+                               % (args.layers, head["inputs_per_layer"]),
+                   "tokens": 1, "top_k": shape.top_k, "hidden": H, "experts": E, "intermediate": I,
                    "bits": 3, "layers_rotated": args.layers},
         "decode_us_per_token_layer": round(head["us_per_layer"], 3),
-        "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "whole layer (all kernels of one call), per-call time"},
+        "roofline": roof,
         "cpu_baseline": cpu,
-        "detail": {**{k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+        "detail": {"measured_copy_GBs": round(copy_gbs, 1),
+                   **{k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in results.items()},
                    **{k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in prefill.items()}},
@@ -191,12 +246,44 @@ def main():
     return 0
 
 
-def cpu_baseline(layer_t, shape, seconds):
+def measured_copy_gbs(torch, dev) -> float:
+    """Read+write bandwidth of a 1 GiB device-to-device copy (a measured ceiling beside the spec)."""
+    a = torch.empty(2 ** 30, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * a.numel() * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+    return gbs
+
+
+def stage1_traffic(bytes_alg: float):
+    """HBM bytes per launch of the decode stage 1 from the committed rocprofv3 counter summary:
+    (FETCH_SIZE + WRITE_SIZE) KiB per dispatch, each divided by the ratio the same counter
+    reads for a device copy of known size."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        fetch = t["fetch_kib_per_dispatch"] * 1024 / t["copy_fetch_ratio"]
+        write = t["write_kib_per_dispatch"] * 1024 / t["copy_write_ratio"]
+        return round(fetch + write)
+    except (OSError, KeyError, ValueError, ZeroDivisionError):
+        return None
+
+
+def cpu_baseline(ex, shape, seconds):
     """Oracle C restatement of the reference expert MLP on this host's cores (T=1, K=8)."""
     import numpy as np
-    import torch
 
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, HERE)
     from oracle import moe_oracle as O
     from kandiga_amd import synth
 
@@ -205,11 +292,7 @@ def cpu_baseline(layer_t, shape, seconds):
     x, logits = synth.make_inputs(shape, ntok, 424242)
     idx, w = O.route(logits, shape.top_k)
     uniq, inv = np.unique(idx, return_inverse=True)
-    ex = torch.as_tensor(uniq.astype(np.int64), device=layer_t["gate_w"].device)
-    sub = {}
-    for k, v in layer_t.items():
-        a = v.index_select(0, ex).cpu().numpy()
-        sub[k] = a.view(np.uint32) if k.endswith("_w") else a.view(np.uint16)
+    sub = ex.host_subset(uniq.astype(np.int64))
     pos = inv.reshape(idx.shape).astype(np.int32)
     log(f"cpu baseline: oracle expert MLP, {threads} threads, up to {seconds:.0f} s")
     O.switch_mlp(sub, x[:1], pos[:1], shape.bits, nthreads=threads)  # warm

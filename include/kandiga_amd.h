@@ -161,6 +161,26 @@ int kmoe_dequantize(const kmoe_layer* layer, int32_t proj, int32_t expert, int32
 /* Synchronise `stream`, then read and clear the device error flags kept in `workspace`. */
 int kmoe_device_status(void* workspace, size_t workspace_bytes, int32_t* flags, void* stream);
 
+/*
+ * Kernel timing.  No counterpart in the reference, whose engine times whole calls on the host;
+ * for benchmarks and profilers.  After kmoe_profile_begin(max_launches), every kernel this
+ * library launches from the calling thread (up to max_launches, at most 16384) is bracketed by
+ * a pair of HIP events recorded on the launch stream; launches into a stream under graph
+ * capture are not timed.  kmoe_profile_end synchronises those events and fills one entry per
+ * kernel name (launch count, total / min / max event time in ms), then stops timing.
+ */
+typedef struct kmoe_kernel_time {
+  char name[48];
+  int32_t launches;
+  int32_t reserved;
+  double total_ms;
+  double min_ms;
+  double max_ms;
+} kmoe_kernel_time;
+
+int kmoe_profile_begin(int32_t max_launches);
+int kmoe_profile_end(kmoe_kernel_time* entries, int32_t max_entries, int32_t* n_entries);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,7 @@ EXPORTS = (
     "kmoe_route", "kmoe_permute_workspace_size", "kmoe_permute",
     "kmoe_expert_mlp", "kmoe_combine", "kmoe_forward",
     "kmoe_dequantize", "kmoe_device_status",
+    "kmoe_profile_begin", "kmoe_profile_end",
 )
 
 OK = 0
@@ -54,6 +55,11 @@ class LayerDesc(ctypes.Structure):
                 ("shared_intermediate", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
+class KernelTime(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 48), ("launches", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("total_ms", ctypes.c_double), ("min_ms", ctypes.c_double), ("max_ms", ctypes.c_double)]
+
+
 _lib = None
 _vp, _i32, _sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
 
@@ -75,6 +81,8 @@ def _declare(L):
         "kmoe_forward": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
         "kmoe_dequantize": ([_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp], ctypes.c_int),
         "kmoe_device_status": ([_vp, _sz, P(_i32), _vp], ctypes.c_int),
+        "kmoe_profile_begin": ([_i32], ctypes.c_int),
+        "kmoe_profile_end": ([P(KernelTime), _i32, P(_i32)], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

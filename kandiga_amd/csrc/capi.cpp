@@ -6,6 +6,7 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "../../include/kandiga_amd.h"
 #include "kmoe_internal.h"
@@ -42,6 +43,27 @@ int hip_fail(hipError_t e, const char* what) {
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Per-thread kernel timing state (kmoe_profile_begin / kmoe_profile_end).
+struct ProfRec {
+  const char* name;
+  hipEvent_t e0, e1;
+};
+struct Prof {
+  bool on = false;
+  hipError_t failed = hipSuccess;
+  std::vector<hipEvent_t> events;
+  std::vector<ProfRec> recs;
+};
+thread_local Prof g_prof;
+
+Prof& prof() { return g_prof; }
+bool prof_on() { return g_prof.on; }
+void prof_reset() {
+  for (hipEvent_t ev : g_prof.events)
+    if (ev) (void)hipEventDestroy(ev);
+  g_prof = Prof{};
+}
 
 int max_mtiles_for(int TK, int E) { return (TK + GEMM_BM - 1) / GEMM_BM + (E < TK ? E : TK); }
 
@@ -80,7 +102,7 @@ Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y32,
   return w;
 }
 
-bool is_decode(int T, int K) { return T <= DEC_MAX_TOKENS && T * K <= DEC_MAX_ASSIGN; }
+bool is_decode(int T, int K) { return T <= DEC_MAX_TOKENS && T * K <= DEC_STAGE2_ASSIGN; }
 
 Work layer_work(const kmoe_layer* L, char* base, int T, size_t* total) {
   const LayerArgs& a = L->cfg.args;
@@ -367,9 +389,79 @@ int kmoe_device_status(void* workspace, size_t workspace_bytes, int32_t* flags, 
   return e == hipSuccess ? ok() : hip_fail(e, "device status");
 }
 
+int kmoe_profile_begin(int32_t max_launches) {
+  if (max_launches < 1 || max_launches > 16384) return fail(KMOE_ERR_INVALID_ARG, "max_launches must be 1..16384");
+  if (prof_on()) return fail(KMOE_ERR_INVALID_ARG, "kernel timing already on for this thread");
+  prof_reset();
+  Prof& p = prof();
+  p.events.resize(2 * (size_t)max_launches, nullptr);
+  for (auto& ev : p.events) {
+    hipError_t e = hipEventCreate(&ev);
+    if (e != hipSuccess) {
+      ev = nullptr;
+      prof_reset();
+      return hip_fail(e, "hipEventCreate");
+    }
+  }
+  p.recs.reserve((size_t)max_launches);
+  p.on = true;
+  return ok();
+}
+
+int kmoe_profile_end(kmoe_kernel_time* entries, int32_t max_entries, int32_t* n_entries) {
+  if (!prof_on()) return fail(KMOE_ERR_INVALID_ARG, "kernel timing is not on for this thread");
+  if (!n_entries || max_entries < 0 || (max_entries > 0 && !entries)) {
+    prof_reset();
+    return fail(KMOE_ERR_INVALID_ARG, "bad output arguments");
+  }
+  Prof& p = prof();
+  std::vector<kmoe_kernel_time> agg;
+  hipError_t err = p.failed;
+  for (const ProfRec& r : p.recs) {
+    if (err != hipSuccess) break;
+    float ms = 0.f;
+    err = hipEventSynchronize(r.e1);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, r.e0, r.e1);
+    if (err != hipSuccess) break;
+    kmoe_kernel_time* t = nullptr;
+    for (auto& a : agg)
+      if (std::strncmp(a.name, r.name, sizeof a.name) == 0) t = &a;
+    if (!t) {
+      kmoe_kernel_time z{};
+      std::snprintf(z.name, sizeof z.name, "%s", r.name);
+      z.min_ms = 1e30;
+      agg.push_back(z);
+      t = &agg.back();
+    }
+    t->launches += 1;
+    t->total_ms += ms;
+    t->min_ms = ms < t->min_ms ? ms : t->min_ms;
+    t->max_ms = ms > t->max_ms ? ms : t->max_ms;
+  }
+  prof_reset();
+  if (err != hipSuccess) return hip_fail(err, "kernel timing events");
+  *n_entries = (int32_t)agg.size();
+  for (int32_t i = 0; i < (int32_t)agg.size() && i < max_entries; ++i) entries[i] = agg[i];
+  return ok();
+}
+
 }  // extern "C"
 
 namespace kmoe {
+
+void prof_events(const char* kernel_name, hipStream_t s, hipEvent_t* start, hipEvent_t* stop) {
+  *start = *stop = nullptr;
+  if (!prof_on()) return;
+  Prof& p = prof();
+  if (p.failed != hipSuccess || p.recs.size() * 2 >= p.events.size()) return;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+  const size_t i = p.recs.size();
+  p.recs.push_back(ProfRec{kernel_name, p.events[2 * i], p.events[2 * i + 1]});
+  *start = p.events[2 * i];
+  *stop = p.events[2 * i + 1];
+}
+
 hipError_t launch_shared(const LayerConfig&, const uint16_t*, int, const Work&, hipStream_t) {
   return hipErrorNotSupported;
 }

@@ -16,8 +16,7 @@
 //     chunk per lane per step), accumulates q*x with v_dot2_f32_f16 on raw codes, applies
 //     s*2^24*dot + b*sum(x) per chunk, reduces across the wave with DPP and writes
 //     act = silu(gate) * up as two fp16 planes (hi, lo: hi + lo carries ~22 bits) in pair
-//     order.  While its loads are in flight it also touches its share of the expert's down
-//     rows, so stage 2 finds them in the memory-side cache.
+//     order.
 //   dec_stage2_kernel: grid = blocks of 64/LPR output rows (LPR lanes per row).  The four
 //     waves split the distinct experts; each lane accumulates w[t,k] * (down row . act) per
 //     token and the waves' partials are added in a fixed order in LDS, so the combine
@@ -27,6 +26,24 @@
 #include "kmoe_internal.h"
 
 namespace kmoe {
+
+// Phase trace, compiled in only with -DKMOE_PHASE_TRACE: thread 0 of each workgroup stores the
+// 100 MHz s_memrealtime clock at the marked points of the two decode kernels, read back with
+// kmoe_phase_trace_dump().  Marks, stage 1: 0 entry, 1 routed, 2 x staged, 3 grouped,
+// 4 item computed, 5 end; stage 2: 0 entry, 1 metadata, 2 experts done, 3 end.
+#ifdef KMOE_PHASE_TRACE
+constexpr int TRACE_WGS = 4096;
+__device__ uint64_t g_phase_trace[2][TRACE_WGS][8];
+#define KMOE_MARK(k, i)                                                  \
+  do {                                                                   \
+    if (threadIdx.x == 0 && blockIdx.x < TRACE_WGS)                      \
+      g_phase_trace[k][blockIdx.x][i] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define KMOE_MARK(k, i) \
+  do {                  \
+  } while (0)
+#endif
 
 template <int BITS>
 struct PairPosTable {
@@ -83,11 +100,8 @@ struct Stage1Args {
   int T, K;
   int32_t* idx_out;         // [T][K] routing (workgroup 0), may be null
   float* w_out;             // [T][K]
-  int32_t* perm;            // grouping for stage 2 (workgroup 0)
-  int32_t* ustart;
-  int32_t* unique;
   int32_t* scalars;         // [0] = distinct experts, [2] = device error flags
-  uint16_t* act;            // [2][T*K][I]
+  uint16_t* act;            // [2][T*K][I], row a = assignment t*K + k
   size_t act_plane;
   int wgs_per_expert;
 };
@@ -110,6 +124,7 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   uint32_t* xs = dyn;                                                  // [T][nch][16]
   float* xsum = reinterpret_cast<float*>(dyn + (size_t)T * nch * 16);  // [T][nch]
   const bool lead = blockIdx.x == 0;
+  KMOE_MARK(0, 0);
 
   // x of every token, pair order, with per-chunk sums.  Each thread's first chunk is loaded
   // before the routing code so its latency overlaps the logits loads.
@@ -131,6 +146,7 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
       s_e[a] = (e >= 0 && e < E) ? e : -1;
     }
   }
+  KMOE_MARK(0, 1);
   for (int task = tid; task < ntask; task += 256) {
     uint32_t nat[16], pr[16];
     if (task == tid) {
@@ -149,69 +165,91 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
     xsum[task] = sm;
   }
   __syncthreads();
-  // stable grouping: rank of (expert, assignment) among the valid assignments
-  const int my_e = tid < TK ? s_e[tid] : -1;
-  if (my_e >= 0) {
-    const int key = my_e * DEC_MAX_ASSIGN + tid;
-    int r = 0;
-    for (int b = 0; b < TK; ++b) {
-      const int eb = s_e[b];
-      r += (eb >= 0) & ((eb * DEC_MAX_ASSIGN + b) < key);
+  KMOE_MARK(0, 2);
+  // stable grouping of the valid assignments by expert: s_perm lists them by (expert, id),
+  // s_unique / s_ustart give each distinct expert and the start of its run
+  int nvalid, nu;
+  if (TK <= 64) {
+    if (wave == 0) {  // one wave, lane a holds assignment a: ranks by a radix pass of ballots
+      const int e = lane < TK ? s_e[lane] : -1;
+      const bool valid = e >= 0;
+      const uint64_t below = (1ull << lane) - 1ull;
+      const int nbits = 32 - __clz(max(E - 1, 1));
+      // eq: valid lanes whose expert agrees with mine on the bits seen so far;
+      // less: valid lanes whose expert is smaller
+      uint64_t eq = __ballot(valid);
+      int less = 0;
+      for (int bit = nbits - 1; bit >= 0; --bit) {
+        const bool one = (e >> bit) & 1;
+        const uint64_t ones = __ballot(valid && one);
+        less += one ? __popcll(eq & ~ones) : 0;
+        eq &= one ? ones : ~ones;
+      }
+      const int r = less + __popcll(eq & below);
+      const bool first = valid && (eq & below) == 0;
+      uint64_t eqf = __ballot(first);
+      int ur = 0;
+      for (int bit = nbits - 1; bit >= 0; --bit) {
+        const bool one = (e >> bit) & 1;
+        const uint64_t ones = __ballot(first && one);
+        ur += one ? __popcll(eqf & ~ones) : 0;
+        eqf &= one ? ones : ~ones;
+      }
+      if (valid) s_perm[r] = lane;
+      if (first) {
+        s_unique[ur] = e;
+        s_ustart[ur] = r;
+      }
+      const int nv = __popcll(__ballot(valid)), nf = __popcll(__ballot(first));
+      if (lane == 0) {
+        s_ustart[nf] = nv;
+        s_tmp[0] = nv;
+        s_tmp[1] = nf;
+      }
     }
-    s_perm[r] = tid;
-  }
-  int nvalid;
-  block_prefix_count(my_e >= 0, s_tmp, &nvalid);  // its barriers also order the s_perm writes
-  int pe = -1;
-  bool first = false;
-  if (tid < nvalid) {
-    pe = s_e[s_perm[tid]];
-    first = tid == 0 || s_e[s_perm[tid - 1]] != pe;
-  }
-  int nu;
-  const int ur = block_prefix_count(first, s_tmp, &nu);
-  if (first) {
-    s_unique[ur] = pe;
-    s_ustart[ur] = tid;
-  }
-  if (tid == 0) s_ustart[nu] = nvalid;
-  __syncthreads();
-  if (lead) {
-    if (tid < nvalid) A.perm[tid] = s_perm[tid];
-    if (tid < nu) A.unique[tid] = s_unique[tid];
-    if (tid <= nu) A.ustart[tid] = s_ustart[tid];
-    if (tid == 0) {
-      A.scalars[0] = nu;
-      if (nvalid != TK) atomicOr(&A.scalars[2], DEVERR_BAD_EXPERT);
+    __syncthreads();
+    nvalid = s_tmp[0];
+    nu = s_tmp[1];
+  } else {
+    const int my_e = tid < TK ? s_e[tid] : -1;
+    if (my_e >= 0) {
+      const int key = my_e * DEC_MAX_ASSIGN + tid;
+      int r = 0;
+      for (int b = 0; b < TK; ++b) {
+        const int eb = s_e[b];
+        r += (eb >= 0) & ((eb * DEC_MAX_ASSIGN + b) < key);
+      }
+      s_perm[r] = tid;
     }
+    block_prefix_count(my_e >= 0, s_tmp, &nvalid);  // its barriers also order the s_perm writes
+    int pe = -1;
+    bool first = false;
+    if (tid < nvalid) {
+      pe = s_e[s_perm[tid]];
+      first = tid == 0 || s_e[s_perm[tid - 1]] != pe;
+    }
+    const int ur = block_prefix_count(first, s_tmp, &nu);
+    if (first) {
+      s_unique[ur] = pe;
+      s_ustart[ur] = tid;
+    }
+    if (tid == 0) s_ustart[nu] = nvalid;
+    __syncthreads();
+  }
+  if (lead && tid == 0) {
+    A.scalars[0] = nu;
+    if (nvalid != TK) atomicOr(&A.scalars[2], DEVERR_BAD_EXPERT);
   }
 
+  KMOE_MARK(0, 3);
   // (expert slot, block of 4*RW rows) items, grid-strided over the workgroups
   const int nitems = nu * A.wgs_per_expert;
-  uint32_t touch = 0;
   for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
   const int u = item / A.wgs_per_expert;
   const int rb = item - u * A.wgs_per_expert;
   const int e = s_unique[u];
   const int p0 = s_ustart[u];
   const int na = min(s_ustart[u + 1] - p0, NT);
-
-  // touch this item's share of expert e's down rows (codes, scales, biases)
-  {
-    const size_t dbytes = (size_t)H * I * BITS / 8;
-    const size_t sbytes = (size_t)H * (I / GROUP) * 2;
-    const size_t dshare = ((dbytes + A.wgs_per_expert - 1) / A.wgs_per_expert + 127) & ~(size_t)127;
-    const size_t sshare = ((sbytes + A.wgs_per_expert - 1) / A.wgs_per_expert + 127) & ~(size_t)127;
-    const uint8_t* dw = L.down.w + (size_t)e * L.down.w_stride;
-    const uint8_t* ds = reinterpret_cast<const uint8_t*>(L.down.s + (size_t)e * L.down.s_stride);
-    const uint8_t* db = reinterpret_cast<const uint8_t*>(L.down.b + (size_t)e * L.down.s_stride);
-    const size_t dend = min(dbytes, (size_t)(rb + 1) * dshare);
-    const size_t send = min(sbytes, (size_t)(rb + 1) * sshare);
-    for (size_t off = (size_t)rb * dshare + (size_t)tid * 128; off < dend; off += 256 * 128)
-      touch += *reinterpret_cast<const uint32_t*>(dw + off);
-    for (size_t off = (size_t)rb * sshare + (size_t)tid * 128; off < send; off += 256 * 128)
-      touch += *reinterpret_cast<const uint32_t*>(ds + off) + *reinterpret_cast<const uint32_t*>(db + off);
-  }
 
   const int ib = rb * (4 * DEC_RW) + wave * DEC_RW;
   const size_t rbytes = (size_t)H * BITS / 8;
@@ -220,9 +258,12 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   const uint8_t* uw = L.up.w + (size_t)e * L.up.w_stride + (size_t)ib * rbytes;
   const size_t gso = (size_t)e * L.gate.s_stride + (size_t)ib * ng;
   const size_t uso = (size_t)e * L.up.s_stride + (size_t)ib * ng;
-  int tok[NT];
+  int asg[NT], tok[NT];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) tok[j] = j < na ? s_perm[p0 + j] / K : 0;
+  for (int j = 0; j < NT; ++j) {
+    asg[j] = j < na ? s_perm[p0 + j] : 0;
+    tok[j] = asg[j] / K;
+  }
 
   float ag[DEC_RW][NT], au[DEC_RW][NT];
 #pragma unroll
@@ -273,136 +314,157 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
           const float a = activate<ACT>(g, uu);
           const _Float16 hi = (_Float16)a;
           const _Float16 lo = (_Float16)(a - (float)hi);
-          const size_t o = (size_t)(p0 + j) * I + (i & ~31) + pairpos<BITS>(i & 31);
+          const size_t o = (size_t)asg[j] * I + (i & ~31) + pairpos<BITS>(i & 31);
           A.act[o] = __builtin_bit_cast(uint16_t, hi);
           A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
         }
       }
     }
   }
+  KMOE_MARK(0, 4);
   }  // item loop
-  // consume the touched words so the loads are kept (the condition is never true)
-  if (touch == 0x9E3779B9u && blockIdx.x == 0x7FFFFFFF) A.scalars[63] = (int32_t)touch;
+  KMOE_MARK(0, 5);
 }
 
-template <int BITS, bool BF16, int NT, bool COMBINE>
+constexpr int S2_ROWS = 8;  // output rows per stage-2 workgroup
+
+// Stage 2.  Lane (g, c) of a wave works on assignment g of its unit and 32-wide chunk c of the
+// intermediate dimension, for RPW consecutive output rows: each act chunk is loaded once per
+// workgroup and reused across the rows.  A unit is (group of 64/LPA assignments, RPW-row
+// subset of the workgroup's S2_ROWS rows); the four waves take units round-robin, UF at a
+// time with all their loads in flight.  Per-assignment row results go to LDS and the combine
+// sums them in k order (moe_block.metal:515-539), so the result does not depend on timing.
+template <int BITS, bool BF16, int RPW, int UF, bool COMBINE>
 __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int T, int K,
-                                                         const int32_t* __restrict__ perm,
-                                                         const int32_t* __restrict__ ustart,
-                                                         const int32_t* __restrict__ unique,
-                                                         const int32_t* __restrict__ scalars,
+                                                         const int32_t* __restrict__ idx,
                                                          const float* __restrict__ wts,
                                                          const uint16_t* __restrict__ act, size_t act_plane,
                                                          void* __restrict__ out, int out32,
-                                                         const float* __restrict__ shared_out, int lpr_log2) {
-  __shared__ int32_t s_perm[DEC_MAX_ASSIGN];
-  __shared__ int32_t s_unique[DEC_MAX_ASSIGN];
-  __shared__ int32_t s_ustart[DEC_MAX_ASSIGN + 1];
-  __shared__ float s_w[DEC_MAX_ASSIGN];
-  __shared__ float red[4 * 32 * 8];
+                                                         const float* __restrict__ shared_out, int lpa_log2) {
+  __shared__ float red[DEC_STAGE2_ASSIGN * S2_ROWS];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int H = L.H, I = L.I, nchI = I / CHUNK;
-  // routing metadata in one round of independent loads (entries past the valid count are unused)
-  const int TK = T * K;
-  __shared__ float s_wa[DEC_MAX_ASSIGN];
-  __shared__ int32_t s_U;
-  if (tid == 0) s_U = scalars[0];
-  const int nuq = min(TK, L.E);  // distinct experts are at most min(T*K, E)
-  for (int q = tid; q <= TK; q += 256) {
-    if (q <= nuq) s_ustart[q] = ustart[q];
-    if (q < nuq) s_unique[q] = unique[q];
-    if (q < TK) {
-      s_perm[q] = perm[q];
-      if (COMBINE) s_wa[q] = wts[q];
-    }
+  const int H = L.H, I = L.I, E = L.E, nchI = I / CHUNK, TK = T * K;
+  KMOE_MARK(1, 0);
+  // routing of assignment a = t*K + k sits in lane a % 64 of slot a / 64 (T*K <= 128)
+  int32_t ev0 = -1, ev1 = -1;
+  float wv0 = 0.f, wv1 = 0.f;
+  if (lane < TK) {
+    ev0 = idx[lane];
+    if (COMBINE) wv0 = wts[lane];
   }
-  __syncthreads();
-  const int U = s_U;
-  const int npos = s_ustart[U];
-  for (int q = tid; q < npos; q += 256) s_w[q] = COMBINE ? s_wa[s_perm[q]] : 0.f;
-  __syncthreads();
+  if (lane + 64 < TK) {
+    ev1 = idx[lane + 64];
+    if (COMBINE) wv1 = wts[lane + 64];
+  }
+  KMOE_MARK(1, 1);
 
-  const int LPR = 1 << lpr_log2, RPS = 64 >> lpr_log2;
-  const int rl = lane >> lpr_log2;
-  const int cl = lane & (LPR - 1);
-  const int h = blockIdx.x * RPS + rl;
+  const int LPA = 1 << lpa_log2, AG = 64 >> lpa_log2;
+  const int g = lane >> lpa_log2;
+  const int cl = lane & (LPA - 1);
+  const int h0 = blockIdx.x * S2_ROWS;
   const size_t rbytes = (size_t)I * BITS / 8;
   const int ng = I / GROUP;
-  float acc[NT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j) acc[j] = 0.f;
+  constexpr int NSUB = S2_ROWS / RPW;
+  const int nunits = ((TK + AG - 1) / AG) * NSUB;
 
-  for (int uu = wave; uu < U; uu += 4) {
-    const int e = s_unique[uu], p0 = s_ustart[uu];
-    const int na = min(s_ustart[uu + 1] - p0, NT);
-    const uint8_t* dw = L.down.w + (size_t)e * L.down.w_stride + (size_t)h * rbytes;
-    const size_t dso = (size_t)e * L.down.s_stride + (size_t)h * ng;
-    float accj[NT];
+  for (int u0 = wave; u0 < nunits; u0 += 4 * UF) {
+    int av[UF], ea[UF], hb[UF];
+    bool va[UF];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) accj[j] = 0.f;
-    for (int c = cl; c < nchI; c += LPR) {
-      uint32_t d[4];
-      load_chunk<BITS>(dw, c, d);
-      const float sc = scale_to_f32<BF16>(L.down.s[dso + (c >> 1)]) * TWO24;
-      const float bi = scale_to_f32<BF16>(L.down.b[dso + (c >> 1)]);
-      uint32_t cp[16];
-      unpack_chunk<BITS, false>(d, cp);
+    for (int i = 0; i < UF; ++i) {
+      const int u = u0 + 4 * i;  // uniform
+      const int grp = u / NSUB;
+      hb[i] = h0 + (u - grp * NSUB) * RPW;
+      const int a = grp * AG + g;
+      // the assignment group never straddles the two slots (AG divides 64)
+      const int e = __shfl(grp * AG < 64 ? ev0 : ev1, a & 63, 64);
+      av[i] = a;
+      va[i] = u < nunits && a < TK && e >= 0 && e < E;
+      ea[i] = va[i] ? e : 0;
+    }
+    float part[UF][RPW];
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        if (j < na) {
-          const int pos = p0 + j;
-          uint32_t xh[16], xl[16];
-          load16(act + (size_t)pos * I + (size_t)c * CHUNK, xh);
-          load16(act + act_plane + (size_t)pos * I + (size_t)c * CHUNK, xl);
+    for (int i = 0; i < UF; ++i)
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) part[i][r] = 0.f;
+    for (int c = cl; c < nchI; c += LPA) {
+      uint32_t d[UF][RPW][4], xh[UF][16], xl[UF][16];
+      uint16_t sc[UF][RPW], bi[UF][RPW];
+#pragma unroll
+      for (int i = 0; i < UF; ++i) {
+        if (va[i]) {
+          const uint8_t* wrow = L.down.w + (size_t)ea[i] * L.down.w_stride + (size_t)hb[i] * rbytes;
+          const size_t so = (size_t)ea[i] * L.down.s_stride + (size_t)hb[i] * ng + (c >> 1);
+#pragma unroll
+          for (int r = 0; r < RPW; ++r) {
+            load_chunk<BITS>(wrow + r * rbytes, c, d[i][r]);
+            sc[i][r] = L.down.s[so + r * ng];
+            bi[i][r] = L.down.b[so + r * ng];
+          }
+          load16(act + (size_t)av[i] * I + (size_t)c * CHUNK, xh[i]);
+          load16(act + act_plane + (size_t)av[i] * I + (size_t)c * CHUNK, xl[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < UF; ++i) {
+        if (va[i]) {
           float sh = 0.f, sl = 0.f;
 #pragma unroll
           for (int m = 0; m < 16; ++m) {
-            sh = fdot2(xh[m], ONE2, sh);
-            sl = fdot2(xl[m], ONE2, sl);
+            sh = fdot2(xh[i][m], ONE2, sh);
+            sl = fdot2(xl[i][m], ONE2, sl);
           }
-          const float part = sc * (chunk_dot(cp, xh) + chunk_dot(cp, xl)) + bi * (sh + sl);
-          if constexpr (COMBINE) {
-            const int t = s_perm[pos] / K;
-            const float wv = s_w[pos] * part;
+          const float xs = sh + sl;
 #pragma unroll
-            for (int tt = 0; tt < NT; ++tt) acc[tt] += tt == t ? wv : 0.f;
-          } else {
-            accj[j] += part;
+          for (int r = 0; r < RPW; ++r) {
+            uint32_t cp[16];
+            unpack_chunk<BITS, false>(d[i][r], cp);
+            const float sf = scale_to_f32<BF16>(sc[i][r]) * TWO24, bf = scale_to_f32<BF16>(bi[i][r]);
+            part[i][r] += sf * (chunk_dot(cp, xh[i]) + chunk_dot(cp, xl[i])) + bf * xs;
           }
         }
       }
     }
-    if constexpr (!COMBINE) {
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        if (j < na) {
-          const float v = group_sum(accj[j], LPR);
-          if (cl == 0) static_cast<uint16_t*>(out)[(size_t)s_perm[p0 + j] * H + h] = f32_to_f16_bits(v);
+    for (int i = 0; i < UF; ++i) {
+      const int a = av[i];
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const float v = group_sum_last(part[i][r], LPA);  // 0 for an assignment with an invalid expert
+        if (cl == LPA - 1 && u0 + 4 * i < nunits && a < TK) {
+          if constexpr (COMBINE) {
+            red[a * S2_ROWS + (hb[i] - h0) + r] = v;
+          } else {
+            static_cast<uint16_t*>(out)[(size_t)a * H + hb[i] + r] = f32_to_f16_bits(v);
+          }
         }
       }
     }
   }
+  KMOE_MARK(1, 2);
   if constexpr (COMBINE) {
-#pragma unroll
-    for (int tt = 0; tt < NT; ++tt) {
-      const float v = group_sum(acc[tt], LPR);
-      if (cl == 0) red[(wave * RPS + rl) * NT + tt] = v;
+    __shared__ float s_wt[DEC_STAGE2_ASSIGN];
+    if (wave == 0) {
+      if (lane < TK) s_wt[lane] = wv0;
+      if (lane + 64 < TK) s_wt[lane + 64] = wv1;
     }
     __syncthreads();
-    if (wave == 0 && cl == 0) {
-      for (int tt = 0; tt < T; ++tt) {
-        float v = red[(0 * RPS + rl) * NT + tt];
-        v += red[(1 * RPS + rl) * NT + tt];
-        v += red[(2 * RPS + rl) * NT + tt];
-        v += red[(3 * RPS + rl) * NT + tt];
-        if (shared_out) v += shared_out[(size_t)tt * H + h];
-        if (out32)
-          static_cast<float*>(out)[(size_t)tt * H + h] = v;
-        else
-          static_cast<uint16_t*>(out)[(size_t)tt * H + h] = f32_to_f16_bits(v);
+    if (tid < T * S2_ROWS) {
+      const int t = tid / S2_ROWS, r = tid - t * S2_ROWS;
+      float v = 0.f;
+      for (int k = 0; k < K; ++k) {
+        const int a = t * K + k;
+        v += s_wt[a] * red[a * S2_ROWS + r];
       }
+      const int h = h0 + r;
+      if (shared_out) v += shared_out[(size_t)t * H + h];
+      if (out32)
+        static_cast<float*>(out)[(size_t)t * H + h] = v;
+      else
+        static_cast<uint16_t*>(out)[(size_t)t * H + h] = f32_to_f16_bits(v);
     }
   }
+  KMOE_MARK(1, 3);
 }
 
 // ---- dequantization check kernel (codes and fp16 weights of a few rows) ------------------
@@ -437,9 +499,23 @@ __global__ void dequant_kernel(const QProj P, int in_dim, int expert, int row0, 
 }
 
 // ---- launchers --------------------------------------------------------------------------
+// Compute units of the current device (queried once per device).
+static int cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 static int nt_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8; }
 
-static int lpr_log2_for(int I) {
+// log2 of the lanes that share one assignment in stage 2: the chunk count rounded up, <= 64.
+static int lpa_log2_for(int I) {
   const int nchI = I / CHUNK;
   int l = 0;
   while ((1 << l) < nchI && l < 6) ++l;
@@ -458,7 +534,7 @@ static hipError_t launch_stage1(KERN k1, int grid, size_t lds, hipStream_t s, co
         hipFuncSetAttribute(reinterpret_cast<const void*>(k1), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (ae != hipSuccess) return ae;
   }
-  hipLaunchKernelGGL(k1, dim3(grid), dim3(256), lds, s, A);
+  KMOE_LAUNCH("dec_stage1_kernel", k1, dim3(grid), dim3(256), (uint32_t)lds, s, A);
   return hipGetLastError();
 }
 
@@ -476,28 +552,30 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   A.K = K;
   A.idx_out = d.idx_out;
   A.w_out = d.w_out;
-  A.perm = w.perm;
-  A.ustart = w.ustart;
-  A.unique = w.unique;
   A.scalars = w.scalars;
   A.act = w.act;
   A.act_plane = (size_t)T * K * L.I;
   A.wgs_per_expert = L.I / (4 * DEC_RW);
-  const int grid1 = min(min(T * K, L.E) * A.wgs_per_expert, 1024);
+  // at most two workgroups per CU: every workgroup repeats the routing and x staging, so
+  // the grid stays resident and loops over the (expert, row block) items instead
+  const int grid1 = min(min(T * K, L.E) * A.wgs_per_expert, 2 * cu_count());
   const size_t lds1 = decode_lds_bytes(c, T);
   hipError_t err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, true>, grid1, lds1, s, A)
                             : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, false>, grid1, lds1, s, A);
   if (err != hipSuccess) return err;
-  const int l2 = lpr_log2_for(L.I);
-  const int rps = 64 >> l2;
+  const int l2 = lpa_log2_for(L.I);
+  constexpr int RPW = NT == 1 ? 4 : 8;
+  constexpr int UF = 2;
+  const int32_t* idx = d.idx_in ? d.idx_in : d.idx_out;
+  const dim3 grid2(L.H / S2_ROWS);
   if (d.combine) {
-    hipLaunchKernelGGL((dec_stage2_kernel<BITS, BF16, NT, true>), dim3(L.H / rps), dim3(256), 0, s, L, T, K, w.perm,
-                       w.ustart, w.unique, w.scalars, d.wts, w.act, A.act_plane, d.out, d.out32,
-                       L.sh_gate ? (const float*)w.shared_out : nullptr, l2);
+    KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, RPW, UF, true>), grid2, dim3(256), 0, s, L, T,
+                K, idx, d.wts, (const uint16_t*)w.act, A.act_plane, d.out, d.out32,
+                L.sh_gate ? (const float*)w.shared_out : (const float*)nullptr, l2);
   } else {
-    hipLaunchKernelGGL((dec_stage2_kernel<BITS, BF16, NT, false>), dim3(L.H / rps), dim3(256), 0, s, L, T, K, w.perm,
-                       w.ustart, w.unique, w.scalars, d.wts, w.act, A.act_plane, d.out, 0, (const float*)nullptr,
-                       l2);
+    KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, RPW, UF, false>), grid2, dim3(256), 0, s, L, T,
+                K, idx, (const float*)nullptr, (const uint16_t*)w.act, A.act_plane, d.out, 0,
+                (const float*)nullptr, l2);
   }
   return hipGetLastError();
 }
@@ -513,7 +591,7 @@ static hipError_t decode_nt(const LayerConfig& c, const DecodeCall& d, hipStream
 }
 
 hipError_t launch_decode(const LayerConfig& c, const DecodeCall& d, hipStream_t s) {
-  if (d.T < 1 || d.T > DEC_MAX_TOKENS || d.T * c.top_k > DEC_MAX_ASSIGN) return hipErrorInvalidValue;
+  if (d.T < 1 || d.T > DEC_MAX_TOKENS || d.T * c.top_k > DEC_STAGE2_ASSIGN) return hipErrorInvalidValue;
 #define KMOE_DEC(B, F, A) decode_nt<B, F, A>(c, d, s)
   if (c.bits == 3) {
     if (c.bf16_scales) return c.act ? KMOE_DEC(3, true, 1) : KMOE_DEC(3, true, 0);
@@ -533,16 +611,26 @@ hipError_t launch_dequantize(const LayerConfig& c, int proj, int expert, int row
   if (tasks == 0) return hipSuccess;
   if (c.bits == 3) {
     if (c.bf16_scales)
-      hipLaunchKernelGGL((dequant_kernel<3, true>), grid, block, 0, s, P, in_dim, expert, row0, nrows, codes, wf16);
+      KMOE_LAUNCH("dequant_kernel", (dequant_kernel<3, true>), grid, block, 0, s, P, in_dim, expert, row0, nrows, codes, wf16);
     else
-      hipLaunchKernelGGL((dequant_kernel<3, false>), grid, block, 0, s, P, in_dim, expert, row0, nrows, codes, wf16);
+      KMOE_LAUNCH("dequant_kernel", (dequant_kernel<3, false>), grid, block, 0, s, P, in_dim, expert, row0, nrows, codes, wf16);
   } else {
     if (c.bf16_scales)
-      hipLaunchKernelGGL((dequant_kernel<4, true>), grid, block, 0, s, P, in_dim, expert, row0, nrows, codes, wf16);
+      KMOE_LAUNCH("dequant_kernel", (dequant_kernel<4, true>), grid, block, 0, s, P, in_dim, expert, row0, nrows, codes, wf16);
     else
-      hipLaunchKernelGGL((dequant_kernel<4, false>), grid, block, 0, s, P, in_dim, expert, row0, nrows, codes, wf16);
+      KMOE_LAUNCH("dequant_kernel", (dequant_kernel<4, false>), grid, block, 0, s, P, in_dim, expert, row0, nrows, codes, wf16);
   }
   return hipGetLastError();
 }
 
 }  // namespace kmoe
+
+#ifdef KMOE_PHASE_TRACE
+extern "C" int kmoe_phase_trace_dump(void* host, size_t bytes) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kmoe::g_phase_trace), bytes, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int kmoe_phase_trace_clear(void) {
+  static uint64_t zero[2 * kmoe::TRACE_WGS * 8];
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(kmoe::g_phase_trace), zero, sizeof zero, 0, hipMemcpyHostToDevice);
+}
+#endif

@@ -209,6 +209,21 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __uint_as_float(dpp_u32<CTRL, ROW_MASK>(__float_as_uint(v)));
 }
 
+// Sum over aligned groups of `width` consecutive lanes (a power of two <= 64) with DPP; the
+// group's last lane holds the total (every lane of the group does for width <= 16).
+__device__ __forceinline__ float group_sum_last(float v, int width) {
+  if (width >= 2) v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  if (width >= 4) v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (width == 8) v += dpp_f32<0x141>(v);  // row_half_mirror: quad q meets quad q^1
+  if (width >= 16) {
+    v += dpp_f32<0x124>(v);  // row_ror:4
+    v += dpp_f32<0x128>(v);  // row_ror:8
+  }
+  if (width >= 32) v += dpp_f32<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  if (width >= 64) v += dpp_f32<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
 // Wave64 sum with DPP: quad_perm [1,0,3,2], [2,3,0,1], row_ror 4, 8 give every lane its row
 // sum; row_bcast 15 (rows 1,3) and row_bcast 31 (rows 2,3) accumulate rows into lane 63.
 // Returns the total in every lane.
@@ -222,28 +237,6 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
 }
 
-__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-  const uint32_t lo = dpp_u32<CTRL, ROW_MASK>((uint32_t)v);
-  const uint32_t hi = dpp_u32<CTRL, ROW_MASK>((uint32_t)(v >> 32));
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// Wave64 maximum of unsigned 64-bit values (0 is the identity), same DPP pattern.
-__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
-  v = max_u64(v, dpp_u64<0xB1>(v));
-  v = max_u64(v, dpp_u64<0x4E>(v));
-  v = max_u64(v, dpp_u64<0x124>(v));
-  v = max_u64(v, dpp_u64<0x128>(v));
-  v = max_u64(v, dpp_u64<0x142, 0xA>(v));
-  v = max_u64(v, dpp_u64<0x143, 0xC>(v));
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-  return ((uint64_t)hi << 32) | lo;
-}
-
 // Orderable key of a router logit: larger logit -> larger key, +0 == -0, NaN below all.
 __device__ __forceinline__ uint32_t logit_key(float v) {
   if (v != v) return 0u;
@@ -252,52 +245,79 @@ __device__ __forceinline__ uint32_t logit_key(float v) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// Top-K of one token's router logits by one wave (moe_block.metal:479-503 semantics): K rounds
-// of a DPP arg-max over the composite key (logit key << 32 | ~index), so equal logits go to the
-// lower index; weights exp(l_k - l_max) / sum_j exp(l_j - l_max), summed in k order.  Each lane
-// holds EPL logits (EPL * 64 >= E) and keeps the best of its remaining keys, so a round is one
-// wave max plus a rescan in the lane that supplied the winner.
+// Inverse of logit_key (the NaN key 0 maps back to a NaN).
+__device__ __forceinline__ float logit_from_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Wave64 maximum of unsigned 32-bit values (0 is the identity), same DPP pattern.
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x124>(v));
+  v = max(v, dpp_u32<0x128>(v));
+  v = max(v, dpp_u32<0x142, 0xA>(v));
+  v = max(v, dpp_u32<0x143, 0xC>(v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Top-K of one token's router logits by one wave (moe_block.metal:479-503 semantics): order by
+// logit descending, equal logits to the lower index; weights exp(l_k - l_max) / sum_j
+// exp(l_j - l_max), summed in k order.  Each lane holds EPL logits (EPL * 64 >= E), sorted once
+// by (key desc, index asc).  A round is a 32-bit DPP max over the lanes' head keys; a ballot
+// finds the lanes holding it, and only when two lanes hold the same logit does a second max
+// over the inverted indices pick the lower index.  The winning lane then pops its head.
+// Index e lives in lane e % 64, so the winner's lane follows from its index.
 // Lanes k < K write idx_out[k] / w_out[k] (either may be null) and sel[k] / selw[k] (may be null).
 template <int EPL>
 __device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int K, int32_t* idx_out,
                                           float* w_out, int32_t* sel, float* selw) {
   const int lane = threadIdx.x & 63;
-  float lv[EPL];
+  uint32_t kh[EPL], ke[EPL];  // key, ~index (larger ~index = lower index); padding: key 0, ~index 0
 #pragma unroll
   for (int m = 0; m < EPL; ++m) {
     const int e = lane + 64 * m;
-    lv[m] = e < E ? row[e] : 0.0f;
+    const float v = e < E ? row[e] : 0.0f;
+    kh[m] = e < E ? logit_key(v) : 0u;
+    ke[m] = e < E ? ~(uint32_t)e : 0u;
   }
-  uint64_t keys[EPL];
-  uint64_t best = 0;
+  // odd-even transposition sort, descending by (key, ~index)
 #pragma unroll
-  for (int m = 0; m < EPL; ++m) {
-    const int e = lane + 64 * m;
-    keys[m] = e < E ? (((uint64_t)logit_key(lv[m]) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e)) : 0ull;
-    best = max_u64(best, keys[m]);
+  for (int pass = 0; pass < EPL; ++pass) {
+#pragma unroll
+    for (int j = pass & 1; j + 1 < EPL; j += 2) {
+      const bool sw = kh[j + 1] > kh[j] || (kh[j + 1] == kh[j] && ke[j + 1] > ke[j]);
+      const uint32_t h0 = kh[j], e0 = ke[j];
+      kh[j] = sw ? kh[j + 1] : h0;
+      ke[j] = sw ? ke[j + 1] : e0;
+      kh[j + 1] = sw ? h0 : kh[j + 1];
+      ke[j + 1] = sw ? e0 : ke[j + 1];
+    }
   }
   int my = 0;
   float my_l = 0.0f;
   for (int k = 0; k < K; ++k) {
-    const uint64_t wb = wave_max_u64_dpp(best);
-    const int e = (int)(0xFFFFFFFFu - (uint32_t)wb);
-    float tv = 0.0f;
-    if (best == wb) {  // only the lane holding the winner: drop it, keep its logit, rescan
-      uint64_t nb = 0;
-#pragma unroll
-      for (int m = 0; m < EPL; ++m) {
-        if (keys[m] == wb) {
-          tv = lv[m];
-          keys[m] = 0ull;
-        }
-        nb = max_u64(nb, keys[m]);
-      }
-      best = nb;
+    const uint32_t m = wave_max_u32_dpp(kh[0]);
+    const uint64_t holders = __ballot(kh[0] == m);
+    uint32_t einv;
+    if (__popcll(holders) == 1) {
+      einv = (uint32_t)__builtin_amdgcn_readlane((int)ke[0], (int)__builtin_ctzll(holders));
+    } else {
+      einv = wave_max_u32_dpp(kh[0] == m ? ke[0] : 0u);
     }
-    const float lk = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(tv), e & 63));
+    const int e = (int)~einv;
+    if (lane == (e & 63)) {  // pop the head
+#pragma unroll
+      for (int j = 0; j + 1 < EPL; ++j) {
+        kh[j] = kh[j + 1];
+        ke[j] = ke[j + 1];
+      }
+      kh[EPL - 1] = 0u;
+      ke[EPL - 1] = 0u;
+    }
     if (lane == k) {
       my = e;
-      my_l = lk;
+      my_l = logit_from_key(m);
     }
   }
   const float l0 = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(my_l)));

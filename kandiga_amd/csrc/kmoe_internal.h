@@ -1,5 +1,6 @@
 // Internal host/device interface between the C ABI (capi.cpp) and the kernel files.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -47,7 +48,8 @@ struct Work {
   int32_t* mt_expert;  // [max_mtiles]
   int32_t* mt_row0;    // [max_mtiles]
   int32_t* mt_rows;    // [max_mtiles]
-  uint16_t* act;       // 2 planes [T*K][I] fp16 (hi, lo), pair order, sorted rows
+  uint16_t* act;       // 2 planes [T*K][I] fp16 (hi, lo), pair order; rows by assignment
+                       // (decode) or by expert-sorted position (grouped GEMM)
   float* y32;          // [T*K][H] fp32 per-assignment expert outputs (GEMM path)
   float* shared_out;     // [T][H] fp32 dense shared-expert output
   uint16_t* shared_act;  // [T][Is] fp16 (pair order) shared-expert SwiGLU output
@@ -56,7 +58,8 @@ struct Work {
 constexpr int PERM_TILE = 1024;   // assignments per permutation tile
 constexpr int GEMM_BM = 128;      // assignment rows per grouped-GEMM tile
 constexpr int DEC_MAX_TOKENS = 8; // largest batch served by the GEMV path
-constexpr int DEC_MAX_ASSIGN = 256;
+constexpr int DEC_MAX_ASSIGN = 256;   // grouping arrays of the decode stage 1
+constexpr int DEC_STAGE2_ASSIGN = 128; // assignments held in two lane slots by decode stage 2
 
 // Device error flag bits (Work::scalars[2]).
 constexpr int DEVERR_BAD_EXPERT = 1;
@@ -76,6 +79,22 @@ struct DecodeCall {
   int out32;
   bool combine;
 };
+
+// Kernel timing hook (kmoe_profile_begin/end).  prof_events hands out the next event pair of
+// the calling thread's timing session for a launch of `kernel_name` on `s`, or two nulls when
+// timing is off or `s` is being captured.  KMOE_LAUNCH passes a pair to hipExtLaunchKernelGGL,
+// which stamps the kernel's own start and end into the events; untimed launches are plain.
+void prof_events(const char* kernel_name, hipStream_t s, hipEvent_t* start, hipEvent_t* stop);
+
+#define KMOE_LAUNCH(NAME, KERNEL, GRID, BLOCK, SHMEM, STREAM, ...)                                  \
+  do {                                                                                             \
+    hipEvent_t kmoe_e0_ = nullptr, kmoe_e1_ = nullptr;                                             \
+    ::kmoe::prof_events(NAME, STREAM, &kmoe_e0_, &kmoe_e1_);                                       \
+    if (kmoe_e0_)                                                                                  \
+      hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, kmoe_e0_, kmoe_e1_, 0, __VA_ARGS__); \
+    else                                                                                           \
+      hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, __VA_ARGS__);                         \
+  } while (0)
 
 // ---- launchers (return hipError_t of the launch) ----------------------------------------
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s);

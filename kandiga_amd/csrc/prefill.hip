@@ -320,17 +320,17 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
                             uint16_t* y16, hipStream_t s) {
   const LayerArgs& L = c.args;
   (void)T;
-  hipLaunchKernelGGL((gemm_gateup_kernel<BITS, BF16, ACT>), dim3(max_mtiles * (L.I / 64)), dim3(256), 0, s, L, x,
-                     c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act);
+  KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT>), dim3(max_mtiles * (L.I / 64)), dim3(256),
+              0, s, L, x, c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int n_ht = (L.H + 127) / 128;
   if (y16) {
-    hipLaunchKernelGGL((gemm_down_kernel<BITS, BF16, true>), dim3(max_mtiles * n_ht), dim3(256), 0, s, L, w.perm,
-                       w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act, (float*)nullptr, y16);
+    KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, true>), dim3(max_mtiles * n_ht), dim3(256), 0, s,
+                L, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act, (float*)nullptr, y16);
   } else {
-    hipLaunchKernelGGL((gemm_down_kernel<BITS, BF16, false>), dim3(max_mtiles * n_ht), dim3(256), 0, s, L, w.perm,
-                       w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act, w.y32, (uint16_t*)nullptr);
+    KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, false>), dim3(max_mtiles * n_ht), dim3(256), 0, s,
+                L, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act, w.y32, (uint16_t*)nullptr);
   }
   return hipGetLastError();
 }
@@ -352,14 +352,14 @@ hipError_t launch_combine(const float* y32, const float* wts, int T, int K, int 
                           void* out, int out32, hipStream_t s) {
   if (T == 0) return hipSuccess;
   const dim3 grid((H / 4 + 255) / 256, T);
-  hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(256), 0, s, y32, wts, K, H, shared, out, out32);
+  KMOE_LAUNCH("combine_kernel", combine_kernel<float>, grid, dim3(256), 0, s, y32, wts, K, H, shared, out, out32);
   return hipGetLastError();
 }
 
 hipError_t launch_combine16(const uint16_t* y16, const float* wts, int T, int K, int H, uint16_t* out, hipStream_t s) {
   if (T == 0) return hipSuccess;
   const dim3 grid((H / 4 + 255) / 256, T);
-  hipLaunchKernelGGL(combine_kernel<uint16_t>, grid, dim3(256), 0, s, y16, wts, K, H, (const float*)nullptr,
+  KMOE_LAUNCH("combine_kernel", combine_kernel<uint16_t>, grid, dim3(256), 0, s, y16, wts, K, H, (const float*)nullptr,
                      (void*)out, 0);
   return hipGetLastError();
 }

@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(
 // ---- launchers --------------------------------------------------------------------------
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s) {
   if (T == 0) return hipSuccess;
-  hipLaunchKernelGGL(route_kernel<0>, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, idx, wts);
+  KMOE_LAUNCH("route_kernel", route_kernel<0>, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, idx, wts);
   return hipGetLastError();
 }
 
@@ -185,11 +185,11 @@ hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& 
   (void)max_mtiles;
   const int ntiles = (TK + PERM_TILE - 1) / PERM_TILE;
   if (ntiles == 0) return hipSuccess;
-  hipLaunchKernelGGL(permute_rank_kernel, dim3(ntiles), dim3(256), (size_t)5 * E * sizeof(int32_t), s, idx, TK, E,
+  KMOE_LAUNCH("permute_rank_kernel", permute_rank_kernel, dim3(ntiles), dim3(256), (size_t)5 * E * sizeof(int32_t), s, idx, TK, E,
                      w.local_rank, w.tile_hist, w.scalars);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(permute_scatter_kernel, dim3(ntiles), dim3(256), 0, s, idx, TK, E, ntiles, w.local_rank,
+  KMOE_LAUNCH("permute_scatter_kernel", permute_scatter_kernel, dim3(ntiles), dim3(256), 0, s, idx, TK, E, ntiles, w.local_rank,
                      w.tile_hist, w.perm, w.counts, w.offsets, w.unique, w.ustart, w.scalars, w.mt_expert,
                      w.mt_row0, w.mt_rows);
   return hipGetLastError();

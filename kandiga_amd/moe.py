@@ -49,6 +49,22 @@ class _Proj:
     scale_stride: int    # bytes between experts
 
 
+def _block_projs(buf: "torch.Tensor", geom: ExpertGeometry, expert_size: int | None = None) -> dict:
+    """Projection descriptors over expert-contiguous blocks (BKEX body layout): expert e's
+    tensor starts at buf + e*expert_size + its offset within the block."""
+    offs = geom.offsets()
+    stride = expert_size or geom.expert_size
+    flat = buf.reshape(-1)
+    projs = {}
+    for name in _PROJS:
+        off_w = offs[f"{name}_proj.weight"]
+        if (flat.data_ptr() + off_w) % (16 if geom.bits == 4 else 4):
+            raise ValueError("expert weight tensor is misaligned")
+        projs[name] = _Proj(flat[off_w:], flat[offs[f"{name}_proj.scales"]:], flat[offs[f"{name}_proj.biases"]:],
+                            stride, stride)
+    return projs
+
+
 class QuantizedExperts:
     """All experts of one layer resident in device memory (MLX affine layout, group 64).
 
@@ -99,21 +115,23 @@ class QuantizedExperts:
     # ---- construction helpers ---------------------------------------------------------
     @classmethod
     def from_stacked(cls, shape: LayerShape, layer: dict, device="cuda", scale_dtype: str = "f16",
-                     activation: str = "swiglu") -> "QuantizedExperts":
-        """From a stacked layer dict (numpy from :func:`synth.make_layer` or torch tensors)."""
-        projs = {}
-        keep = []
+                     activation: str = "swiglu", layout: str = "expert") -> "QuantizedExperts":
+        """From a stacked layer dict (numpy from :func:`synth.make_layer` or torch tensors).
+
+        ``layout="expert"`` (default) packs each expert's nine tensors into one contiguous
+        block at the BKEX offsets, as a ``layer_XX.bin`` body holds them
+        (kandiga/metal/kandiga_cpu_expert.m:42-65): one expert then spans at most two 2 MiB
+        pages, which keeps address translation cheap when a decode step touches a few
+        experts out of hundreds.  ``layout="stacked"`` keeps one tensor per projection part
+        (expert stride = one expert's slice)."""
+        if layout not in ("expert", "stacked"):
+            raise ValueError(f"unknown layout {layout!r}")
+        tensors = {}
         for name in _PROJS:
-            ts = []
             for key in ("w", "s", "b"):
                 a = layer[f"{name}_{key}"]
                 t = a if isinstance(a, torch.Tensor) else torch.from_numpy(a.view(a.dtype.str.replace("u", "i")))
-                t = t.to(device).contiguous()
-                ts.append(t)
-            w, s, b = ts
-            projs[name] = _Proj(w, _as_u16(s), _as_u16(b), w[0].numel() * w.element_size(),
-                                s[0].numel() * s.element_size())
-            keep += ts
+                tensors[(name, key)] = t.to(device).contiguous()
         shared = None
         if shape.shared_intermediate and "shared_gate" in layer:
             shared = {}
@@ -121,7 +139,23 @@ class QuantizedExperts:
                 a = layer[f"shared_{name}"]
                 t = a if isinstance(a, torch.Tensor) else torch.from_numpy(a.view("i2"))
                 shared[name] = t.to(device).contiguous()
-        return cls(shape, projs, scale_dtype, activation, shared, keep)
+        if layout == "stacked":
+            projs = {}
+            for name in _PROJS:
+                w, s, b = (tensors[(name, k)] for k in ("w", "s", "b"))
+                projs[name] = _Proj(w, _as_u16(s), _as_u16(b), w[0].numel() * w.element_size(),
+                                    s[0].numel() * s.element_size())
+            return cls(shape, projs, scale_dtype, activation, shared, list(tensors.values()))
+        geom = ExpertGeometry(shape.hidden, shape.intermediate, shape.bits)
+        offs, E = geom.offsets(), shape.num_experts
+        body = torch.empty((E, geom.expert_size), dtype=torch.uint8, device=device)
+        for name in _PROJS:
+            for key, part in (("w", "weight"), ("s", "scales"), ("b", "biases")):
+                t = tensors[(name, key)].reshape(E, -1).view(torch.uint8)
+                off = offs[f"{name}_proj.{part}"]
+                body[:, off:off + t.shape[1]] = t
+        del tensors
+        return cls(shape, _block_projs(body, geom), scale_dtype, activation, shared, [body])
 
     @classmethod
     def from_bkex(cls, path: str, top_k: int, device="cuda", activation: str | None = None) -> "QuantizedExperts":
@@ -136,19 +170,9 @@ class QuantizedExperts:
         if body.size != hdr.num_experts * hdr.expert_size:
             raise ValueError(f"{path}: truncated BKEX body")
         buf = torch.from_numpy(body).to(device)
-        offs = geom.offsets()
         shape = LayerShape(hdr.hidden, hdr.intermediate, hdr.num_experts, top_k, hdr.bits)
-        projs = {}
-        for name in _PROJS:
-            base = buf.data_ptr()
-            w = buf[offs[f"{name}_proj.weight"]:]
-            s = buf[offs[f"{name}_proj.scales"]:]
-            b = buf[offs[f"{name}_proj.biases"]:]
-            if (base + offs[f"{name}_proj.weight"]) % (16 if hdr.bits == 4 else 4):
-                raise ValueError("BKEX weight tensor is misaligned")
-            projs[name] = _Proj(w, s, b, hdr.expert_size, hdr.expert_size)
         act = activation or ("gelu_tanh" if hdr.intermediate == 704 else "swiglu")
-        return cls(shape, projs, hdr.scale_dtype, act, None, [buf])
+        return cls(shape, _block_projs(buf, geom, hdr.expert_size), hdr.scale_dtype, act, None, [buf])
 
     # ---- workspace --------------------------------------------------------------------
     def workspace_bytes(self, tokens: int) -> int:
@@ -166,6 +190,27 @@ class QuantizedExperts:
     def workspace(self, tokens: int) -> torch.Tensor:
         self.reserve(tokens)
         return self._ws
+
+    def host_subset(self, experts) -> dict:
+        """Host copies of the given experts' tensors, stacked in the listed order, as the dict of
+        numpy arrays (``gate_w`` uint32, ``gate_s`` / ``gate_b`` uint16, ...) that
+        :func:`synth.make_layer` produces.  Works for either weight layout."""
+        import numpy as np
+
+        geom = ExpertGeometry(self.shape.hidden, self.shape.intermediate, self.shape.bits)
+        ids = [int(e) for e in experts]
+        out = {}
+        for name, shape, kind, nbytes in geom.tensor_nbytes():
+            proj, part = name.split("_proj.")
+            p = self.projs[proj]
+            base = p.weight if part == "weight" else p.scales if part == "scales" else p.biases
+            stride = p.weight_stride if part == "weight" else p.scale_stride
+            flat = base.reshape(-1).view(torch.uint8)
+            rows = [flat[e * stride:e * stride + nbytes] for e in ids]
+            a = torch.stack(rows).cpu().numpy()
+            key = f"{proj}_{part[0]}"
+            out[key] = a.view(np.uint32 if kind == "w" else np.uint16).reshape((len(ids),) + tuple(shape))
+        return out
 
     def device_status(self) -> int:
         """Read and clear the device error flags (synchronises the current stream)."""
@@ -317,3 +362,33 @@ def combine(y: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
     _capi.check(_capi.lib().kmoe_combine(yy.data_ptr(), ww.data_ptr(), T, K, H, out.data_ptr(), _stream()),
                 "kmoe_combine")
     return out.reshape(*y.shape[:-2], H)
+
+
+class profile_kernels:
+    """Time every kernel the library launches from this thread inside the ``with`` block.
+
+    Each launch is bracketed by a HIP event pair on its stream (kmoe_profile_begin/end), so
+    use it around eager calls, not graph capture.  ``result`` maps kernel name to a dict of
+    launches, total_ms, mean_ms, min_ms, max_ms.
+    """
+
+    def __init__(self, max_launches: int = 4096):
+        self.max_launches = int(max_launches)
+        self.result: dict = {}
+
+    def __enter__(self) -> "profile_kernels":
+        _capi.check(_capi.lib().kmoe_profile_begin(self.max_launches), "kmoe_profile_begin")
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> None:
+        buf = (_capi.KernelTime * 64)()
+        n = ctypes.c_int32()
+        rc = _capi.lib().kmoe_profile_end(buf, 64, ctypes.byref(n))
+        if exc_type is None:
+            _capi.check(rc, "kmoe_profile_end")
+        for i in range(min(n.value, 64)):
+            t = buf[i]
+            self.result[t.name.decode()] = dict(launches=t.launches, total_ms=t.total_ms,
+                                                mean_ms=t.total_ms / max(t.launches, 1), min_ms=t.min_ms,
+                                                max_ms=t.max_ms)
+

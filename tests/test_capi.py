@@ -128,6 +128,15 @@ def test_calls_validate_before_launch():
     L.kmoe_layer_destroy(h)
 
 
+def test_kernel_timing_validates_arguments():
+    L = _capi.lib()
+    assert L.kmoe_profile_begin(0) == _capi.ERR_INVALID_ARG
+    assert L.kmoe_profile_begin(16385) == _capi.ERR_INVALID_ARG
+    n = ctypes.c_int32()
+    assert L.kmoe_profile_end(None, 0, ctypes.byref(n)) == _capi.ERR_INVALID_ARG  # timing is not on
+    assert ctypes.sizeof(_capi.KernelTime) == 80
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_capi, "_lib", None)
     monkeypatch.setattr(_capi, "LIB_PATH", str(tmp_path / "libkandiga_amd.so"))

@@ -123,6 +123,44 @@ def test_forward_small(device, name, T):
     assert_close(to_np(out32), ref["out"], what=f"{name} T={T} layer fp32 out")
 
 
+@pytest.mark.parametrize("layout", ["expert", "stacked"])
+@pytest.mark.parametrize("T", [1, 8, 300])
+def test_forward_both_weight_layouts(device, layout, T):
+    """Expert-contiguous blocks (BKEX body) and one-tensor-per-part stacks give the same layer."""
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+
+    shape = SMALL["3bit-h320-i192"]
+    layer = synth.make_layer(shape, 51)
+    ex = QuantizedExperts.from_stacked(shape, layer, device, layout=layout)
+    x, logits = synth.make_inputs(shape, T, 52 + T)
+    out = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device),
+                             out_dtype=torch.float32)
+    ref = O.moe_layer(layer, x, logits, shape.top_k, shape.bits)
+    assert_close(to_np(out), ref["out"], what=f"{layout} T={T}")
+    sub = ex.host_subset([3, 0, 11])
+    for k, v in sub.items():
+        assert np.array_equal(v, layer[k][[3, 0, 11]]), k
+
+
+def test_kernel_timing_covers_decode_and_prefill(device):
+    from kandiga_amd.moe import SparseMoeBlock, profile_kernels
+
+    shape = SMALL["3bit"]
+    _layer, ex = _experts(shape, 61, device)
+    blk = SparseMoeBlock(ex)
+    ins = [tuple(torch.from_numpy(a).to(device) for a in synth.make_inputs(shape, T, 62 + T)) for T in (1, 300)]
+    ref = [blk(*a) for a in ins]
+    with profile_kernels(64) as prof:
+        got = [blk(*a) for a in ins]
+    for r, g in zip(ref, got):
+        assert torch.equal(r, g)
+    names = ("dec_stage1_kernel", "dec_stage2_kernel", "route_kernel", "permute_rank_kernel",
+             "permute_scatter_kernel", "gemm_gateup_kernel", "gemm_down_kernel", "combine_kernel")
+    for n in names:
+        assert prof.result[n]["launches"] == 1, n
+        assert 0 < prof.result[n]["mean_ms"] < 100, n
+
+
 def test_forward_bf16_scales_gelu(device):
     from kandiga_amd.moe import SparseMoeBlock
 
