@@ -57,6 +57,9 @@ def parse():
     p.add_argument("--modes", default="graph,eager", help="decode launch modes")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run 5 device copies of 256 MiB (the known-size kernel that the "
+                        "FETCH_SIZE / WRITE_SIZE counters are calibrated against) and exit")
     return p.parse_args()
 
 
@@ -67,6 +70,15 @@ def main():
               file=sys.stderr)
         return 2
     import torch
+
+    if args.copy_calibration:
+        a = torch.ones(256 * 2 ** 20, dtype=torch.uint8, device="cuda:0")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": a.numel(), "copies": 5}), flush=True)
+        return 0
 
     from kandiga_amd import synth
     from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock, profile_kernels
