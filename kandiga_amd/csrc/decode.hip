@@ -326,6 +326,152 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   KMOE_MARK(0, 5);
 }
 
+// Stage 1 for a single token.  Wave 0 routes the token (or every wave reads the given indices)
+// and shares the K experts through LDS behind the kernel's one barrier; every wave keeps the x
+// chunks its lanes multiply in registers (pair order, with chunk sums), so x is not staged in
+// LDS.  Lane k < K of each wave holds assignment k's expert.  The distinct experts are the lanes whose expert no lower lane also holds (routing
+// never repeats one; given indices may), and each (distinct expert, block of 4*RW rows) item
+// writes act for every assignment of that expert.  CPL = x chunks per lane (H <= 64*32*CPL).
+template <int BITS, bool BF16, int ACT, int CPL, bool ROUTE>
+__global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) {
+  const LayerArgs& L = A.L;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int K = A.K, H = L.H, I = L.I, E = L.E;
+  const int nch = H / CHUNK;
+  KMOE_MARK(0, 0);
+  uint32_t xr[CPL][16];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      load16(A.x + (size_t)c * CHUNK, xr[j]);
+    } else {
+#pragma unroll
+      for (int m = 0; m < 16; ++m) xr[j][m] = 0u;
+    }
+  }
+  int my = -1;
+  if constexpr (ROUTE) {
+    // one routing wave per workgroup: redundant copies in the other waves would share SIMDs
+    // with it and stretch its latency; they wait at the barrier instead
+    __shared__ int32_t s_sel[16];
+    if (wave == 0) {
+      float myw;
+      KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(A.logits, E, K, my, myw)));
+      if (lane < K) {
+        s_sel[lane] = my;
+        if (blockIdx.x == 0) {
+          if (A.idx_out) A.idx_out[lane] = my;
+          if (A.w_out) A.w_out[lane] = myw;
+        }
+      }
+    }
+    __syncthreads();
+    my = lane < K ? s_sel[lane] : -1;
+  } else {
+    if (lane < K) {
+      const int e = A.idx_in[lane];
+      my = (e >= 0 && e < E) ? e : -1;
+    }
+  }
+  KMOE_MARK(0, 1);
+  uint32_t xp[CPL][16];
+  float xs[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    to_pair_order<BITS>(xr[j], xp[j]);
+    float sm = 0.f;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) sm = fdot2(xr[j][m], ONE2, sm);
+    xs[j] = sm;
+  }
+  KMOE_MARK(0, 2);
+  const uint64_t valid_m = __ballot(my >= 0);
+  bool first = my >= 0;
+  if constexpr (!ROUTE) {
+    for (int j = 0; j < K; ++j) {
+      const int ej = __builtin_amdgcn_readlane(my, j);
+      first = first && !(j < lane && ej == my);
+    }
+  }
+  const uint64_t first_m = __ballot(first);
+  const int nu = __popcll(first_m);
+  if (blockIdx.x == 0 && tid == 0) {
+    A.scalars[0] = nu;
+    if (__popcll(valid_m) != K) atomicOr(&A.scalars[2], DEVERR_BAD_EXPERT);
+  }
+  KMOE_MARK(0, 3);
+
+  const int nitems = nu * A.wgs_per_expert;
+  const size_t rbytes = (size_t)H * BITS / 8;
+  const int ng = H / GROUP;
+  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+    const int u = item / A.wgs_per_expert;
+    const int rb = item - u * A.wgs_per_expert;
+    uint64_t fm = first_m;
+    for (int q = 0; q < u; ++q) fm &= fm - 1ull;
+    const int e = __builtin_amdgcn_readlane(my, (int)__builtin_ctzll(fm));
+    const uint64_t amask = __ballot(my == e);
+    const int ib = rb * (4 * DEC_RW) + wave * DEC_RW;
+    const uint8_t* gw = L.gate.w + (size_t)e * L.gate.w_stride + (size_t)ib * rbytes;
+    const uint8_t* uw = L.up.w + (size_t)e * L.up.w_stride + (size_t)ib * rbytes;
+    const size_t gso = (size_t)e * L.gate.s_stride + (size_t)ib * ng;
+    const size_t uso = (size_t)e * L.up.s_stride + (size_t)ib * ng;
+    uint32_t gd[CPL][DEC_RW][4], ud[CPL][DEC_RW][4];
+    uint16_t gsc[CPL][DEC_RW], gbi[CPL][DEC_RW], usc[CPL][DEC_RW], ubi[CPL][DEC_RW];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nch) {
+#pragma unroll
+        for (int r = 0; r < DEC_RW; ++r) {
+          load_chunk<BITS>(gw + r * rbytes, c, gd[j][r]);
+          load_chunk<BITS>(uw + r * rbytes, c, ud[j][r]);
+          gsc[j][r] = L.gate.s[gso + r * ng + (c >> 1)];
+          gbi[j][r] = L.gate.b[gso + r * ng + (c >> 1)];
+          usc[j][r] = L.up.s[uso + r * ng + (c >> 1)];
+          ubi[j][r] = L.up.b[uso + r * ng + (c >> 1)];
+        }
+      }
+    }
+    float ag[DEC_RW], au[DEC_RW];
+#pragma unroll
+    for (int r = 0; r < DEC_RW; ++r) ag[r] = au[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      if (lane + 64 * j < nch) {
+#pragma unroll
+        for (int r = 0; r < DEC_RW; ++r) {
+          uint32_t cg[16], cu[16];
+          unpack_chunk<BITS, false>(gd[j][r], cg);
+          unpack_chunk<BITS, false>(ud[j][r], cu);
+          ag[r] += scale_to_f32<BF16>(gsc[j][r]) * TWO24 * chunk_dot(cg, xp[j]) + scale_to_f32<BF16>(gbi[j][r]) * xs[j];
+          au[r] += scale_to_f32<BF16>(usc[j][r]) * TWO24 * chunk_dot(cu, xp[j]) + scale_to_f32<BF16>(ubi[j][r]) * xs[j];
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < DEC_RW; ++r) {
+      const float g = wave_sum_dpp(ag[r]);
+      const float uu = wave_sum_dpp(au[r]);
+      if (lane == 0) {
+        const int i = ib + r;
+        const float a = activate<ACT>(g, uu);
+        const _Float16 hi = (_Float16)a;
+        const _Float16 lo = (_Float16)(a - (float)hi);
+        const size_t col = (size_t)(i & ~31) + pairpos<BITS>(i & 31);
+        for (uint64_t m = amask; m; m &= m - 1ull) {
+          const size_t o = (size_t)__builtin_ctzll(m) * I + col;
+          A.act[o] = __builtin_bit_cast(uint16_t, hi);
+          A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
+        }
+      }
+    }
+    KMOE_MARK(0, 4);
+  }
+  KMOE_MARK(0, 5);
+}
+
 constexpr int S2_ROWS = 8;  // output rows per stage-2 workgroup
 
 // Stage 2.  Lane (g, c) of a wave works on assignment g of its unit and 32-wide chunk c of the
@@ -560,8 +706,19 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   // the grid stays resident and loops over the (expert, row block) items instead
   const int grid1 = min(min(T * K, L.E) * A.wgs_per_expert, 2 * cu_count());
   const size_t lds1 = decode_lds_bytes(c, T);
-  hipError_t err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, true>, grid1, lds1, s, A)
-                            : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, false>, grid1, lds1, s, A);
+  const int nch = L.H / CHUNK;
+  hipError_t err;
+  if (NT == 1 && nch <= 128) {
+    if (nch <= 64)
+      err = d.logits ? launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 1, true>, grid1, 0, s, A)
+                     : launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 1, false>, grid1, 0, s, A);
+    else
+      err = d.logits ? launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 2, true>, grid1, 0, s, A)
+                     : launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 2, false>, grid1, 0, s, A);
+  } else {
+    err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, true>, grid1, lds1, s, A)
+                   : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, false>, grid1, lds1, s, A);
+  }
   if (err != hipSuccess) return err;
   const int l2 = lpa_log2_for(L.I);
   constexpr int RPW = NT == 1 ? 4 : 8;

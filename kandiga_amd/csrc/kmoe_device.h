@@ -268,10 +268,9 @@ __device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
 // finds the lanes holding it, and only when two lanes hold the same logit does a second max
 // over the inverted indices pick the lower index.  The winning lane then pops its head.
 // Index e lives in lane e % 64, so the winner's lane follows from its index.
-// Lanes k < K write idx_out[k] / w_out[k] (either may be null) and sel[k] / selw[k] (may be null).
+// Lane k < K returns the k-th expert in `sel` and its weight in `selw`; other lanes get -1, 0.
 template <int EPL>
-__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int K, int32_t* idx_out,
-                                          float* w_out, int32_t* sel, float* selw) {
+__device__ __forceinline__ void wave_topk_regs(const float* __restrict__ row, int E, int K, int& sel, float& selw) {
   const int lane = threadIdx.x & 63;
   uint32_t kh[EPL], ke[EPL];  // key, ~index (larger ~index = lower index); padding: key 0, ~index 0
 #pragma unroll
@@ -325,11 +324,23 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, 
   float sum = 0.0f;
   for (int k = 0; k < K; ++k)
     sum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(ex), k));
+  sel = lane < K ? my : -1;
+  selw = lane < K ? ex / sum : 0.0f;
+}
+
+// wave_topk_regs with the results stored: lanes k < K write idx_out[k] / w_out[k] (either may
+// be null) and sel[k] / selw[k] (may be null).
+template <int EPL>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int K, int32_t* idx_out,
+                                          float* w_out, int32_t* sel, float* selw) {
+  const int lane = threadIdx.x & 63;
+  int e;
+  float w;
+  wave_topk_regs<EPL>(row, E, K, e, w);
   if (lane < K) {
-    const float w = ex / sum;
-    if (idx_out) idx_out[lane] = my;
+    if (idx_out) idx_out[lane] = e;
     if (w_out) w_out[lane] = w;
-    if (sel) sel[lane] = my;
+    if (sel) sel[lane] = e;
     if (selw) selw[lane] = w;
   }
 }
