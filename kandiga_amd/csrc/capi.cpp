@@ -68,7 +68,7 @@ void prof_reset() {
 int max_mtiles_for(int TK, int E) { return (TK + GEMM_BM - 1) / GEMM_BM + (E < TK ? E : TK); }
 
 // Carve the workspace for `T` tokens.  base == nullptr computes the size only.
-Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y32, size_t* total) {
+Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y, size_t* total) {
   Work w{};
   size_t off = 0;
   auto take = [&](size_t bytes) -> char* {
@@ -93,7 +93,7 @@ Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y32,
   w.mt_row0 = reinterpret_cast<int32_t*>(take((size_t)mmt * 4));
   w.mt_rows = reinterpret_cast<int32_t*>(take((size_t)mmt * 4));
   w.act = reinterpret_cast<uint16_t*>(take(TK * I * 2 * 2));  // hi and lo planes
-  if (need_y32) w.y32 = reinterpret_cast<float*>(take(TK * H * 4));
+  if (need_y) w.y32 = reinterpret_cast<float*>(take(TK * H * 4));
   if (Is > 0) {
     w.shared_out = reinterpret_cast<float*>(take((size_t)T * H * 4));
     w.shared_act = reinterpret_cast<uint16_t*>(take((size_t)T * Is * 2));
@@ -307,7 +307,7 @@ int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, 
   } else {
     const int mmt = max_mtiles_for(tokens * K, c.args.E);
     e = launch_permute(idx, tokens * K, K, c.args.E, w, mmt, s);
-    if (e == hipSuccess) e = launch_gemm(c, xx, tokens, w, mmt, yy, s);
+    if (e == hipSuccess) e = launch_gemm(c, xx, tokens, w, mmt, yy, nullptr, s);
   }
   return e == hipSuccess ? ok() : hip_fail(e, "expert_mlp launch");
 }
@@ -320,8 +320,8 @@ int kmoe_combine(const void* y, const float* weights, int32_t tokens, int32_t to
   if (!y || !weights || !out) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
   if (!aligned(y, 8) || !aligned(out, 8) || !aligned(weights, 4))
     return fail(KMOE_ERR_ALIGNMENT, "y/out must be 8-byte aligned, weights 4-byte aligned");
-  hipError_t e = launch_combine16(static_cast<const uint16_t*>(y), weights, tokens, top_k, hidden,
-                                  static_cast<uint16_t*>(out), static_cast<hipStream_t>(stream));
+  hipError_t e = launch_combine(nullptr, static_cast<const uint16_t*>(y), weights, tokens, top_k, hidden, nullptr,
+                                out, 0, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? ok() : hip_fail(e, "combine launch");
 }
 
@@ -358,9 +358,10 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
     const int mmt = max_mtiles_for(tokens * K, a.E);
     e = launch_route(logits, tokens, a.E, K, w.idx, w.wts, s);
     if (e == hipSuccess) e = launch_permute(w.idx, tokens * K, K, a.E, w, mmt, s);
-    if (e == hipSuccess) e = launch_gemm(c, xx, tokens, w, mmt, nullptr, s);
+    if (e == hipSuccess) e = launch_gemm(c, xx, tokens, w, mmt, nullptr, w.wts, s);
     if (e == hipSuccess)
-      e = launch_combine(w.y32, w.wts, tokens, K, a.H, a.sh_gate ? w.shared_out : nullptr, out, out32, s);
+      e = launch_combine(w.y32, nullptr, nullptr, tokens, K, a.H, a.sh_gate ? w.shared_out : nullptr, out, out32,
+                         s);
   }
   return e == hipSuccess ? ok() : hip_fail(e, "forward launch");
 }

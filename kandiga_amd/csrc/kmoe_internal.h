@@ -50,7 +50,7 @@ struct Work {
   int32_t* mt_rows;    // [max_mtiles]
   uint16_t* act;       // 2 planes [T*K][I] fp16 (hi, lo), pair order; rows by assignment
                        // (decode) or by expert-sorted position (grouped GEMM)
-  float* y32;          // [T*K][H] fp32 per-assignment expert outputs (GEMM path)
+  float* y32;          // [T*K][H] fp32 weighted per-assignment outputs (grouped-GEMM path of forward)
   float* shared_out;     // [T][H] fp32 dense shared-expert output
   uint16_t* shared_act;  // [T][Is] fp16 (pair order) shared-expert SwiGLU output
 };
@@ -100,12 +100,13 @@ void prof_events(const char* kernel_name, hipStream_t s, hipEvent_t* start, hipE
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s);
 hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, hipStream_t s);
 hipError_t launch_decode(const LayerConfig& c, const DecodeCall& d, hipStream_t s);
+// Per-assignment outputs: y16 (fp16, unweighted: the switch_mlp contract) or, when y16 is
+// null, Work::y32 (fp32, each row scaled by its routing weight in wscale for the combine).
 hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Work& w, int max_mtiles,
-                       uint16_t* y16, hipStream_t s);
-hipError_t launch_combine(const float* y32, const float* wts, int T, int K, int H, const float* shared,
-                          void* out, int out32, hipStream_t s);
-hipError_t launch_combine16(const uint16_t* y16, const float* wts, int T, int K, int H, uint16_t* out,
-                            hipStream_t s);
+                       uint16_t* y16, const float* wscale, hipStream_t s);
+// out[t] = sum_k (wts ? wts[t,k] : 1) * y[t,k] (+ shared[t]); y is fp32 (y32) or fp16 bits (y16).
+hipError_t launch_combine(const float* y32, const uint16_t* y16, const float* wts, int T, int K, int H,
+                          const float* shared, void* out, int out32, hipStream_t s);
 hipError_t launch_shared(const LayerConfig& c, const uint16_t* x, int T, const Work& w, hipStream_t s);
 hipError_t launch_dequantize(const LayerConfig& c, int proj, int expert, int row0, int nrows, uint8_t* codes,
                              uint16_t* wf16, hipStream_t s);
