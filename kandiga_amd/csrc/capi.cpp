@@ -93,7 +93,10 @@ Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y, s
   w.mt_row0 = reinterpret_cast<int32_t*>(take((size_t)mmt * 4));
   w.mt_rows = reinterpret_cast<int32_t*>(take((size_t)mmt * 4));
   w.act = reinterpret_cast<uint16_t*>(take(TK * I * 2 * 2));  // hi and lo planes
-  if (need_y) w.y32 = reinterpret_cast<float*>(take(TK * H * 4));
+  if (need_y) {
+    w.y32 = reinterpret_cast<float*>(take(TK * H * 4));
+    w.xpp = reinterpret_cast<uint16_t*>(take((size_t)T * H * 2));
+  }
   if (Is > 0) {
     w.shared_out = reinterpret_cast<float*>(take((size_t)T * H * 4));
     w.shared_act = reinterpret_cast<uint16_t*>(take((size_t)T * Is * 2));
@@ -307,7 +310,8 @@ int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, 
   } else {
     const int mmt = max_mtiles_for(tokens * K, c.args.E);
     e = launch_permute(idx, tokens * K, K, c.args.E, w, mmt, s);
-    if (e == hipSuccess) e = launch_gemm(c, xx, tokens, w, mmt, yy, nullptr, s);
+    if (e == hipSuccess) e = launch_xpair(c, xx, tokens, w.xpp, s);
+    if (e == hipSuccess) e = launch_gemm(c, w.xpp, tokens, w, mmt, yy, nullptr, s);
   }
   return e == hipSuccess ? ok() : hip_fail(e, "expert_mlp launch");
 }
@@ -358,7 +362,8 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
     const int mmt = max_mtiles_for(tokens * K, a.E);
     e = launch_route(logits, tokens, a.E, K, w.idx, w.wts, s);
     if (e == hipSuccess) e = launch_permute(w.idx, tokens * K, K, a.E, w, mmt, s);
-    if (e == hipSuccess) e = launch_gemm(c, xx, tokens, w, mmt, nullptr, w.wts, s);
+    if (e == hipSuccess) e = launch_xpair(c, xx, tokens, w.xpp, s);
+    if (e == hipSuccess) e = launch_gemm(c, w.xpp, tokens, w, mmt, nullptr, w.wts, s);
     if (e == hipSuccess)
       e = launch_combine(w.y32, nullptr, nullptr, tokens, K, a.H, a.sh_gate ? w.shared_out : nullptr, out, out32,
                          s);

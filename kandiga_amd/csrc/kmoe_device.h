@@ -77,30 +77,43 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t s0, uint32_t s1, uint32_t 
 }
 
 // 3-bit chunk (dwords d0..d2, codes c_j at bits 3j of the 96-bit stream) -> 16 pairs.
+// (v & M) | O in one v_and_or_b32 when O != 0.  gfx9 VOP3 encodes no literal and reads at most
+// one SGPR, so M goes in an SGPR and O in a VGPR (both loop-invariant).
+template <uint32_t M, uint32_t O>
+__device__ __forceinline__ uint32_t mask_or(uint32_t v) {
+  if constexpr (O == 0u) {
+    return v & M;
+  } else {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(M), "v"(O));
+    return r;
+  }
+}
+
 template <bool MAGIC>
 __device__ __forceinline__ void unpack3(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t (&p)[16]) {
   constexpr uint32_t M = 0x00070007u, O = MAGIC ? 0x64006400u : 0u;
-  p[0] = (pk_shr(d0, 0, 2) & M) | O;
-  p[1] = (pk_shr(d0, 3, 5) & M) | O;
-  p[2] = (pk_shr(d0, 6, 8) & M) | O;
-  p[3] = (pk_shr(d0, 9, 11) & M) | O;
-  p[4] = (pk_shr(d1, 1, 0) & M) | O;
-  p[5] = (pk_shr(d1, 4, 3) & M) | O;
-  p[6] = (pk_shr(d1, 7, 6) & M) | O;
-  p[7] = (pk_shr(d1, 10, 9) & M) | O;
-  p[8] = (pk_shr(d1, 13, 12) & M) | O;
-  p[9] = (pk_shr(d2, 2, 1) & M) | O;
-  p[10] = (pk_shr(d2, 5, 4) & M) | O;
-  p[11] = (pk_shr(d2, 8, 7) & M) | O;
-  p[12] = (pk_shr(d2, 11, 10) & M) | O;
+  p[0] = mask_or<M, O>(pk_shr(d0, 0, 2));
+  p[1] = mask_or<M, O>(pk_shr(d0, 3, 5));
+  p[2] = mask_or<M, O>(pk_shr(d0, 6, 8));
+  p[3] = mask_or<M, O>(pk_shr(d0, 9, 11));
+  p[4] = mask_or<M, O>(pk_shr(d1, 1, 0));
+  p[5] = mask_or<M, O>(pk_shr(d1, 4, 3));
+  p[6] = mask_or<M, O>(pk_shr(d1, 7, 6));
+  p[7] = mask_or<M, O>(pk_shr(d1, 10, 9));
+  p[8] = mask_or<M, O>(pk_shr(d1, 13, 12));
+  p[9] = mask_or<M, O>(pk_shr(d2, 2, 1));
+  p[10] = mask_or<M, O>(pk_shr(d2, 5, 4));
+  p[11] = mask_or<M, O>(pk_shr(d2, 8, 7));
+  p[12] = mask_or<M, O>(pk_shr(d2, 11, 10));
   // c4: d0 bits 12..14 (low half); c31: d2 bits 29..31 (high half, relative 13)
-  p[13] = (pk_shr((d0 & 0xFFFFu) | (d2 & 0xFFFF0000u), 12, 13) & M) | O;
+  p[13] = mask_or<M, O>(pk_shr((d0 & 0xFFFFu) | (d2 & 0xFFFF0000u), 12, 13));
   // c5: d0 bits 15..17; c26: d2 bits 14..16.  Bytes [d0.b1 d0.b2 | d2.b1 d2.b2] put them at 7 / 6.
-  p[14] = (pk_shr(perm_b32(d2, d0, 0x06050201u), 7, 6) & M) | O;
+  p[14] = mask_or<M, O>(pk_shr(perm_b32(d2, d0, 0x06050201u), 7, 6));
   // c10: stream bits 30..32; c21: stream bits 63..65.
   const uint32_t c10 = __builtin_amdgcn_alignbit(d1, d0, 30);
   const uint32_t c21 = __builtin_amdgcn_alignbit(d2, d1, 31);
-  p[15] = (perm_b32(c21, c10, 0x05040100u) & M) | O;
+  p[15] = mask_or<M, O>(perm_b32(c21, c10, 0x05040100u));
 }
 
 // 4-bit chunk (dwords d0..d3, nibble n of dword j = code 8j+n) -> 16 pairs.
@@ -110,7 +123,7 @@ __device__ __forceinline__ void unpack4(const uint32_t (&d)[4], uint32_t (&p)[16
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[4 * j + i] = ((d[j] >> (4 * i)) & M) | O;
+    for (int i = 0; i < 4; ++i) p[4 * j + i] = mask_or<M, O>(d[j] >> (4 * i));
   }
 }
 

@@ -51,6 +51,7 @@ struct Work {
   uint16_t* act;       // 2 planes [T*K][I] fp16 (hi, lo), pair order; rows by assignment
                        // (decode) or by expert-sorted position (grouped GEMM)
   float* y32;          // [T*K][H] fp32 weighted per-assignment outputs (grouped-GEMM path of forward)
+  uint16_t* xpp;       // [T][H] x in pair order (grouped-GEMM path)
   float* shared_out;     // [T][H] fp32 dense shared-expert output
   uint16_t* shared_act;  // [T][Is] fp16 (pair order) shared-expert SwiGLU output
 };
@@ -100,6 +101,8 @@ void prof_events(const char* kernel_name, hipStream_t s, hipEvent_t* start, hipE
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s);
 hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, hipStream_t s);
 hipError_t launch_decode(const LayerConfig& c, const DecodeCall& d, hipStream_t s);
+// x [T][H] -> xpp in pair order (per 32-wide chunk), the gate/up GEMM's A layout.
+hipError_t launch_xpair(const LayerConfig& c, const uint16_t* x, int T, uint16_t* xpp, hipStream_t s);
 // Per-assignment outputs: y16 (fp16, unweighted: the switch_mlp contract) or, when y16 is
 // null, Work::y32 (fp32, each row scaled by its routing weight in wscale for the combine).
 hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Work& w, int max_mtiles,

@@ -5,9 +5,10 @@
 // scatter back to [T, K, H]) and its 3-bit fallback (engine.py:720-735: T sequential
 // CPU calls).
 //
+//   xpair_kernel: x into pair order once per call (the k order the dequantized weights have).
 //   gemm_gateup_kernel: one workgroup per (m-tile of <= 128 sorted assignments of one
 //     expert, 64 intermediate columns).  Per 64-wide k step the workgroup gathers the
-//     tile's x rows (token = assignment / K) into LDS in pair order, dequantizes the 64
+//     tile's x rows (token = assignment / K, already in pair order) into LDS, dequantizes the 64
 //     gate rows and 64 up rows of that k step into LDS as fp16 (one quant group per row,
 //     round(q*s + b) by one fp16 fma), and runs v_mfma_f32_32x32x16_f16.  Each wave owns
 //     64 rows x 32 columns of both gate and up, so SwiGLU is applied in registers and
@@ -129,6 +130,18 @@ struct KStage {
   uint16_t s, b;
 };
 
+// x [T][H] -> pair order within each 32-wide chunk (the k order of the dequantized weights).
+template <int BITS>
+__global__ __launch_bounds__(256) void xpair_kernel(const uint16_t* __restrict__ x, size_t nchunks,
+                                                    uint16_t* __restrict__ xpp) {
+  const size_t c = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= nchunks) return;
+  uint32_t nat[16], pr[16];
+  load16g(x + c * CHUNK, nat);
+  to_pair_order<BITS>(nat, pr);
+  store16s(reinterpret_cast<_Float16*>(xpp + c * CHUNK), pr);
+}
+
 template <int BITS, bool BF16, int ACT>
 __global__ __launch_bounds__(256, 3) void gemm_gateup_kernel(const LayerArgs L, const uint16_t* __restrict__ x,
                                                              int K, const int32_t* __restrict__ perm,
@@ -175,22 +188,17 @@ __global__ __launch_bounds__(256, 3) void gemm_gateup_kernel(const LayerArgs L, 
 #pragma unroll
       for (int qq = 0; qq < 16; ++qq) acc[i][j][qq] = 0.f;
 
+  // rows past the end of the tile read token 0's x (their results are never stored)
   auto load = [&](KStage& S, int k0) {
-    if (a_ok) {
-      load16g(xrow + k0 + lc * CHUNK, S.a);
-    } else {
-#pragma unroll
-      for (int qq = 0; qq < 16; ++qq) S.a[qq] = 0u;
-    }
+    load16g(xrow + k0 + lc * CHUNK, S.a);
     load_chunk_c<BITS>(wrow, (k0 >> 5) + lc, S.w);
     S.s = srow[k0 >> 6];
     S.b = bsrow[k0 >> 6];
   };
   auto store = [&](const KStage& S) {
-    uint32_t pa[16], pb[16];
-    to_pair_order<BITS>(S.a, pa);
+    uint32_t pb[16];
     dequant_regs<BITS, BF16>(S.w, S.s, S.b, pb);
-    store16s(sA + lr * LDH + lc * CHUNK, pa);
+    store16s(sA + lr * LDH + lc * CHUNK, S.a);
     store16s(sB + lr * LDH + lc * CHUNK, pb);
   };
   auto mma = [&]() {
@@ -290,13 +298,9 @@ __global__ __launch_bounds__(256, 3) void gemm_down_kernel(const LayerArgs L, co
 #pragma unroll
       for (int qq = 0; qq < 16; ++qq) acc[i][j][qq] = 0.f;
 
+  // rows past the end of the tile read the tile's first act row (their results are never stored)
   auto load = [&](KStage& S, int k0) {
-    if (a_ok) {
-      load16g(arow + k0 + lc * CHUNK, S.a);
-    } else {
-#pragma unroll
-      for (int qq = 0; qq < 16; ++qq) S.a[qq] = 0u;
-    }
+    load16g(arow + k0 + lc * CHUNK, S.a);
     load_chunk_c<BITS>(wrow, (k0 >> 5) + lc, S.w);
     S.s = srow[k0 >> 6];
     S.b = bsrow[k0 >> 6];
@@ -446,6 +450,18 @@ hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Wor
   if (c.bf16_scales)
     return c.act ? gemm_impl<4, true, 1>(c, x, T, w, max_mtiles, y16, wscale, s) : gemm_impl<4, true, 0>(c, x, T, w, max_mtiles, y16, wscale, s);
   return c.act ? gemm_impl<4, false, 1>(c, x, T, w, max_mtiles, y16, wscale, s) : gemm_impl<4, false, 0>(c, x, T, w, max_mtiles, y16, wscale, s);
+}
+
+hipError_t launch_xpair(const LayerConfig& c, const uint16_t* x, int T, uint16_t* xpp, hipStream_t s) {
+  const size_t nchunks = (size_t)T * c.args.H / CHUNK;
+  if (nchunks == 0) return hipSuccess;
+  const dim3 grid((unsigned)((nchunks + 255) / 256));
+  if (c.bits == 3) {
+    KMOE_LAUNCH("xpair_kernel", xpair_kernel<3>, grid, dim3(256), 0, s, x, nchunks, xpp);
+  } else {
+    KMOE_LAUNCH("xpair_kernel", xpair_kernel<4>, grid, dim3(256), 0, s, x, nchunks, xpp);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_combine(const float* y32, const uint16_t* y16, const float* wts, int T, int K, int H,
