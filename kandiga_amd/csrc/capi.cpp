@@ -99,7 +99,7 @@ Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y, s
   }
   if (Is > 0) {
     w.shared_out = reinterpret_cast<float*>(take((size_t)T * H * 4));
-    w.shared_act = reinterpret_cast<uint16_t*>(take((size_t)T * Is * 2));
+    w.shared_act = reinterpret_cast<uint16_t*>(take((size_t)T * Is * 4));  // two fp16 planes (decode)
   }
   *total = off;
   return w;
@@ -184,7 +184,6 @@ int kmoe_layer_create(const kmoe_layer_desc* d, kmoe_layer** out) {
       return fail(KMOE_ERR_INVALID_ARG, "shared_intermediate must be a positive multiple of 64");
     if (!aligned(d->shared_gate, 16) || !aligned(d->shared_up, 16) || !aligned(d->shared_down, 16))
       return fail(KMOE_ERR_ALIGNMENT, "shared expert weights must be 16-byte aligned");
-    return fail(KMOE_ERR_UNSUPPORTED, "shared expert not available in this build");
   }
   kmoe_layer* L = new (std::nothrow) kmoe_layer;
   if (!L) return fail(KMOE_ERR_NO_MEMORY, "out of host memory");
@@ -468,7 +467,4 @@ void prof_events(const char* kernel_name, hipStream_t s, hipEvent_t* start, hipE
   *stop = p.events[2 * i + 1];
 }
 
-hipError_t launch_shared(const LayerConfig&, const uint16_t*, int, const Work&, hipStream_t) {
-  return hipErrorNotSupported;
-}
 }  // namespace kmoe

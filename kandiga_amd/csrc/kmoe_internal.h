@@ -53,7 +53,7 @@ struct Work {
   float* y32;          // [T*K][H] fp32 weighted per-assignment outputs (grouped-GEMM path of forward)
   uint16_t* xpp;       // [T][H] x in pair order (grouped-GEMM path)
   float* shared_out;     // [T][H] fp32 dense shared-expert output
-  uint16_t* shared_act;  // [T][Is] fp16 (pair order) shared-expert SwiGLU output
+  uint16_t* shared_act;  // shared-expert SwiGLU output: 2 fp16 planes [T][Is] (decode) or 1 (prefill)
 };
 
 constexpr int PERM_TILE = 1024;   // assignments per permutation tile

@@ -271,6 +271,47 @@ def test_wide_layer_h4096_e512_k10(device):
         assert_close(to_np(out)[rows], O.combine(y, w[rows]), what=f"h4096 e512 T={T}")
 
 
+@pytest.mark.parametrize("T", [1, 3, 8, 9, 200])
+def test_forward_with_shared_expert_small(device, T):
+    """Dense fp16 shared expert added after the routed combine (decode GEMVs and prefill GEMMs)."""
+    from kandiga_amd.moe import SparseMoeBlock
+
+    shape = synth.LayerShape(256, 128, 16, 4, 3, shared_intermediate=192)
+    layer, ex = _experts(shape, 71, device)
+    x, logits = synth.make_inputs(shape, T, 72 + T, zipf=T > 50)
+    ref = O.moe_layer(layer, x, logits, shape.top_k, shape.bits)
+    blk = SparseMoeBlock(ex)
+    xt, lt = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
+    out32 = to_np(blk(xt, lt, out_dtype=torch.float32))
+    assert_close(out32, ref["out"], what=f"shared T={T} fp32 out")
+    assert_close(to_np(blk(xt, lt)), ref["out"], what=f"shared T={T}")
+    # the shared term itself: layer output minus the oracle's routed part
+    routed = O.combine(O.switch_mlp(layer, x, ref["idx"], 3), ref["w"]).astype(np.float64)
+    shared = O.shared_expert_f64(layer, x)
+    assert np.abs(shared).max() > 1e-2
+    np.testing.assert_allclose(out32 - routed, shared, rtol=0, atol=1e-3)
+
+
+def test_hidden2560_layer_with_shared_expert(device):
+    """H=2560, E=256, I=1024, K=8, 3-bit + fp16 shared expert I=1024; oracle on sampled tokens."""
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+
+    shape = synth.SHAPES["h2560-e256-i1024-k8-3bit-shared1024"]
+    layer_t = synth.make_layer_torch(shape, 6001, device)
+    ex = QuantizedExperts.from_stacked(shape, layer_t, device)
+    for T, zipf in ((1, False), (8, False), (2048, True)):
+        x, logits = synth.make_inputs(shape, T, 6100 + T, zipf=zipf)
+        out = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device),
+                                 out_dtype=torch.float32)
+        idx, w = O.route(logits, shape.top_k)
+        rows = np.arange(T) if T <= 8 else np.random.default_rng(T).choice(T, 12, replace=False)
+        uniq, pos = remap(idx[rows])
+        sub = torch_layer_subset(layer_t, uniq)
+        y = O.switch_mlp(sub, x[rows], pos, 3, nthreads=8)
+        ref = (O.combine(y, w[rows]).astype(np.float64) + O.shared_expert_f64(sub, x[rows])).astype(np.float32)
+        assert_close(to_np(out)[rows], ref, what=f"h2560 shared T={T}")
+
+
 def test_decode_graph_replays_match_eager(device):
     """Several replays of a captured stack of decode layers, with eager work between them,
     each bit-identical to the eager result (the fused kernel resets its own counters)."""
