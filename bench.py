@@ -57,6 +57,10 @@ def parse():
     p.add_argument("--modes", default="graph,eager", help="decode launch modes")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--no-shared-layer", dest="shared_layer", action="store_false",
+                   help="skip the hidden-2560 layer with the dense shared expert")
+    p.add_argument("--stack60", action="store_true",
+                   help="also run the 60-layer hidden-4096 / 512-expert / top-10 stack (~169 GB resident)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 5 device copies of 256 MiB (the known-size kernel that the "
                         "FETCH_SIZE / WRITE_SIZE counters are calibrated against) and exit")
@@ -86,7 +90,6 @@ def main():
     dev = torch.device("cuda:0")
     shape = synth.SHAPES["h2048-e256-i512-k8-3bit"]
     H, E, I = shape.hidden, shape.num_experts, shape.intermediate
-    gu_bytes = 2 * I * H * 3 // 8 + 4 * I * (H // 64) * 2   # gate + up codes, scales, biases
     log(f"generating {args.layers} layers of {shape.name} ({shape.expert_bytes * E / 2**20:.0f} MiB each)")
     layers = [synth.make_layer_torch(shape, 7000 + i, dev) for i in range(args.layers)]
     experts = {k: [QuantizedExperts.from_stacked(shape.with_top_k(k), L, dev) for L in layers] for k in (8, 4)}
@@ -96,17 +99,21 @@ def main():
     copy_gbs = measured_copy_gbs(torch, dev)
     log(f"device copy: {copy_gbs:.0f} GB/s (read + write)")
 
-    def decode_case(T, k, graph):
-        blocks = [SparseMoeBlock(ex) for ex in experts[k]]
-        for ex in experts[k]:
+    def decode_case(T, k, graph, exs=None, shp=None, profile=True):
+        exs = exs if exs is not None else experts[k]
+        shp = shp or shape
+        H, E, I = shp.hidden, shp.num_experts, shp.intermediate
+        gu_bytes = 2 * I * H * shp.bits // 8 + 4 * I * (H // 64) * 2
+        blocks = [SparseMoeBlock(ex) for ex in exs]
+        for ex in exs:
             ex.reserve(T)
         L = len(blocks)
-        est = min(T * k, E) * shape.expert_bytes
-        P = max(2, math.ceil(ROTATE_BYTES / (L * est)))
+        est = min(T * k, E) * shp.expert_bytes
+        P = max(1 if L >= 32 else 2, math.ceil(ROTATE_BYTES / (L * est)))
         seq = []  # (block, x, logits) in call order: every layer with input set 0, then set 1, ...
         for p in range(P):
             for li, b in enumerate(blocks):
-                x, lg = synth.make_inputs_torch(shape, T, 9000 + 997 * p + 31 * li + T, dev)
+                x, lg = synth.make_inputs_torch(shp, T, 9000 + 997 * p + 31 * li + T, dev)
                 seq.append((li, b, x, lg))
         b_alg, b_s1, uniq, seen = [], [], [], [set() for _ in blocks]
         for li, b, x, lg in seq:
@@ -115,9 +122,9 @@ def main():
             U = len(ids)
             seen[li].update(ids)
             uniq.append(U)
-            b_alg.append(U * shape.expert_bytes + T * H * 2 + T * E * 4 + T * H * 2 + T * k * 8)
+            b_alg.append(U * shp.expert_bytes + shp.shared_bytes + T * H * 2 + T * E * 4 + T * H * 2 + T * k * 8)
             b_s1.append(U * gu_bytes + T * H * 2 + T * E * 4 + T * k * I * 4 + T * k * 8)
-        distinct = sum(len(s) for s in seen) * shape.expert_bytes
+        distinct = sum(len(s) for s in seen) * shp.expert_bytes
         outs = [None] * len(seq)
         if graph:
             g = torch.cuda.CUDAGraph()
@@ -153,7 +160,7 @@ def main():
         r = dict(T=T, k=k, us_per_layer=us, gbs=ba / (us * 1e-6) / 1e9, bytes_alg=ba,
                  unique_experts=sum(uniq) / n, calls=reps * n, inputs_per_layer=P,
                  distinct_expert_bytes_per_replay=distinct)
-        if graph:
+        if graph and profile:
             # per-kernel event timing over one eager pass of the same calls
             with profile_kernels(4 * n + 16) as prof:
                 for _li, b, x, lg in seq:
@@ -180,36 +187,70 @@ def main():
             log(f"{key}: {r['us_per_layer']:.2f} us/layer  {r['gbs']:.0f} GB/s  U={r['unique_experts']:.1f} "
                 f"P={r['inputs_per_layer']} distinct={r['distinct_expert_bytes_per_replay'] / 2**30:.2f} GiB{extra}")
 
-    prefill = {}
-    ptoks = [int(v) for v in args.prefill.split(",") if v]
-    if ptoks:
-        ex = experts[8][0]
+    def prefill_case(ex, shp, T, tag=""):
         blk = SparseMoeBlock(ex)
-        for T in ptoks:
-            x, lg = synth.make_inputs_torch(shape, T, 12000 + T, dev, zipf=True)
-            ex.reserve(T)
+        H, I = shp.hidden, shp.intermediate
+        x, lg = synth.make_inputs_torch(shp, T, 12000 + T, dev, zipf=True)
+        ex.reserve(T)
+        for _ in range(3):
+            blk(x, lg)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.prefill_steps):
+            blk(x, lg)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / args.prefill_steps
+        with profile_kernels(64) as prof:
             for _ in range(3):
                 blk(x, lg)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(args.prefill_steps):
-                blk(x, lg)
-            e1.record()
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / args.prefill_steps
-            with profile_kernels(64) as prof:
-                for _ in range(3):
-                    blk(x, lg)
-            kern = {n: round(v["mean_ms"] * 1e3, 2) for n, v in prof.result.items()}
-            flops = 2.0 * T * shape.top_k * 3 * H * I
-            gemm_us = kern.get("gemm_gateup_kernel", 0) + kern.get("gemm_down_kernel", 0)
-            prefill[f"prefill_T{T}"] = dict(
-                T=T, us=us, tokens_per_s=T / (us * 1e-6), tflops=flops / (us * 1e-6) / 1e12,
-                mfma_frac=flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, kernel_us=kern,
-                gemm_mfma_frac=(flops / (gemm_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS) if gemm_us else None)
-            log(f"prefill T={T}: {us:.1f} us  {T / (us * 1e-6) / 1e6:.2f} M tok/s  "
-                f"{flops / (us * 1e-6) / 1e12:.1f} TFLOP/s  kernels(us) {kern}")
+        kern = {n: round(v["mean_ms"] * 1e3, 2) for n, v in prof.result.items()}
+        flops = 2.0 * T * shp.top_k * 3 * H * I + 2.0 * T * 3 * H * shp.shared_intermediate
+        gemm_us = kern.get("gemm_gateup_kernel", 0) + kern.get("gemm_down_kernel", 0)
+        r = dict(T=T, us=us, tokens_per_s=T / (us * 1e-6), tflops=flops / (us * 1e-6) / 1e12,
+                 mfma_frac=flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, kernel_us=kern,
+                 gemm_mfma_frac=(2.0 * T * shp.top_k * 3 * H * I / (gemm_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS)
+                 if gemm_us else None)
+        log(f"prefill{tag} T={T}: {us:.1f} us  {T / (us * 1e-6) / 1e6:.2f} M tok/s  "
+            f"{flops / (us * 1e-6) / 1e12:.1f} TFLOP/s  kernels(us) {kern}")
+        return r
+
+    prefill = {}
+    for T in [int(v) for v in args.prefill.split(",") if v]:
+        prefill[f"prefill_T{T}"] = prefill_case(experts[8][0], shape, T)
+
+    # the hidden-2560 layer with a dense fp16 shared expert (decode over 4 rotated layers)
+    if args.shared_layer:
+        shp4 = synth.SHAPES["h2560-e256-i1024-k8-3bit-shared1024"]
+        log(f"generating 4 layers of {shp4.name}")
+        ex4 = [QuantizedExperts.from_stacked(shp4, synth.make_layer_torch(shp4, 7100 + i, dev), dev)
+               for i in range(4)]
+        torch.cuda.synchronize()
+        for T in (1, 8):
+            r = decode_case(T, 8, True, ex4, shp4, profile=False)
+            results[f"shared_layer_decode_T{T}_K8_graph"] = r
+            log(f"{shp4.name} decode T={T}: {r['us_per_layer']:.2f} us/layer  {r['gbs']:.0f} GB/s (incl. shared "
+                f"expert bytes)")
+        prefill["shared_layer_prefill_T2048"] = prefill_case(ex4[0], shp4, 2048, " (hidden 2560 + shared)")
+        del ex4
+        torch.cuda.empty_cache()
+
+    # 60 independent hidden-4096 / 512-expert / top-10 layers resident (~169 GB): one decode
+    # token through the whole stack per replay
+    if args.stack60:
+        shp5 = synth.SHAPES["h4096-e512-i1024-k10-3bit"]
+        log(f"generating 60 layers of {shp5.name} ({shp5.expert_bytes * shp5.num_experts * 60 / 1e9:.0f} GB)")
+        ex5 = [QuantizedExperts.from_stacked(shp5, synth.make_layer_torch(shp5, 7200 + i, dev), dev)
+               for i in range(60)]
+        torch.cuda.synchronize()
+        r = decode_case(1, 10, True, ex5, shp5, profile=False)
+        r["us_per_token_60_layers"] = r["us_per_layer"] * 60
+        results["stack60_decode_T1_K10_graph"] = r
+        log(f"60-layer {shp5.name} stack, decode T=1: {r['us_per_layer']:.2f} us/layer, "
+            f"{r['us_per_layer'] * 60:.1f} us/token, {r['gbs']:.0f} GB/s")
+        del ex5
+        torch.cuda.empty_cache()
 
     head = results.get("decode_T1_K8_graph") or next(iter(results.values()), None)
     if head is None:
