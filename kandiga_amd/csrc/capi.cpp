@@ -105,11 +105,12 @@ Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y, s
   return w;
 }
 
-bool is_decode(int T, int K) { return T <= DEC_MAX_TOKENS && T * K <= DEC_STAGE2_ASSIGN; }
+// GEMV decode kernels: up to 8 tokens, 128 assignments, hidden <= 4096 (two x chunks per lane).
+bool is_decode(int T, int K, int H) { return T <= DEC_MAX_TOKENS && T * K <= DEC_STAGE2_ASSIGN && H <= 4096; }
 
 Work layer_work(const kmoe_layer* L, char* base, int T, size_t* total) {
   const LayerArgs& a = L->cfg.args;
-  return carve(base, T, L->cfg.top_k, a.E, a.H, a.I, a.sh_gate ? a.Is : 0, !is_decode(T, L->cfg.top_k), total);
+  return carve(base, T, L->cfg.top_k, a.E, a.H, a.I, a.sh_gate ? a.Is : 0, !is_decode(T, L->cfg.top_k, L->cfg.args.H), total);
 }
 
 int check_qproj(const kmoe_qproj& q, const char* name, int rows, int in, int bits, int E) {
@@ -303,7 +304,7 @@ int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, 
   const uint16_t* xx = static_cast<const uint16_t*>(x);
   uint16_t* yy = static_cast<uint16_t*>(y);
   hipError_t e;
-  if (is_decode(tokens, K)) {
+  if (is_decode(tokens, K, c.args.H)) {
     DecodeCall d{xx, nullptr, idx, tokens, nullptr, nullptr, nullptr, &w, yy, 0, false};
     e = launch_decode(c, d, s);
   } else {
@@ -354,7 +355,7 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
   hipError_t e = hipSuccess;
   if (a.sh_gate) e = launch_shared(c, xx, tokens, w, s);
   if (e != hipSuccess) return hip_fail(e, "shared expert launch");
-  if (is_decode(tokens, K)) {
+  if (is_decode(tokens, K, a.H)) {
     DecodeCall d{xx, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true};
     e = launch_decode(c, d, s);
   } else {

@@ -69,7 +69,10 @@ __device__ __forceinline__ int pairpos(int e) {
 
 constexpr float TWO24 = 16777216.0f;
 constexpr uint32_t ONE2 = 0x3C003C00u;  // fp16 pair (1, 1)
-constexpr int DEC_RW = 2;               // gate/up row pairs per wave step
+constexpr int DEC_RW = 2;               // gate/up rows per wave per item of the single-token stage 1
+// Gate/up rows per wave per item of the multi-token stage 1: more rows per item keep more
+// weight bytes in flight per wave once several experts are selected.
+constexpr int stage1_rw(int nt) { return nt >= 4 ? 4 : 2; }
 
 template <int ACT>
 __device__ __forceinline__ float activate(float g, float u) {
@@ -106,7 +109,7 @@ struct Stage1Args {
   int wgs_per_expert;
 };
 
-template <int BITS, bool BF16, int ACT, int NT, bool ROUTE>
+template <int BITS, bool BF16, int ACT, int NT, int CPL, bool ROUTE>
 __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   extern __shared__ uint32_t dyn[];
   __shared__ int32_t s_e[DEC_MAX_ASSIGN];
@@ -242,87 +245,113 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   }
 
   KMOE_MARK(0, 3);
-  // (expert slot, block of 4*RW rows) items, grid-strided over the workgroups
+  // (expert slot, block of 4*RW rows) items, grid-strided over the workgroups.  The weights of
+  // the next item are loaded while the current one is computed (two register stages,
+  // unrolled by two so no stage is copied while its loads are in flight).
+  constexpr int RW = stage1_rw(NT);
   const int nitems = nu * A.wgs_per_expert;
-  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
-  const int u = item / A.wgs_per_expert;
-  const int rb = item - u * A.wgs_per_expert;
-  const int e = s_unique[u];
-  const int p0 = s_ustart[u];
-  const int na = min(s_ustart[u + 1] - p0, NT);
-
-  const int ib = rb * (4 * DEC_RW) + wave * DEC_RW;
   const size_t rbytes = (size_t)H * BITS / 8;
   const int ng = H / GROUP;
-  const uint8_t* gw = L.gate.w + (size_t)e * L.gate.w_stride + (size_t)ib * rbytes;
-  const uint8_t* uw = L.up.w + (size_t)e * L.up.w_stride + (size_t)ib * rbytes;
-  const size_t gso = (size_t)e * L.gate.s_stride + (size_t)ib * ng;
-  const size_t uso = (size_t)e * L.up.s_stride + (size_t)ib * ng;
-  int asg[NT], tok[NT];
+  struct WStage {
+    uint32_t gd[CPL][RW][4], ud[CPL][RW][4];
+    uint16_t gsc[CPL][RW], gbi[CPL][RW], usc[CPL][RW], ubi[CPL][RW];
+  };
+  auto load_item = [&](int item, WStage& W) {
+    const int u = item / A.wgs_per_expert;
+    const int rb = item - u * A.wgs_per_expert;
+    const int e = s_unique[u];
+    const int ib = rb * (4 * RW) + wave * RW;
+    const uint8_t* gw = L.gate.w + (size_t)e * L.gate.w_stride + (size_t)ib * rbytes;
+    const uint8_t* uw = L.up.w + (size_t)e * L.up.w_stride + (size_t)ib * rbytes;
+    const size_t gso = (size_t)e * L.gate.s_stride + (size_t)ib * ng;
+    const size_t uso = (size_t)e * L.up.s_stride + (size_t)ib * ng;
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    asg[j] = j < na ? s_perm[p0 + j] : 0;
-    tok[j] = asg[j] / K;
-  }
-
-  float ag[DEC_RW][NT], au[DEC_RW][NT];
+    for (int q = 0; q < CPL; ++q) {
+      const int c = min(lane + 64 * q, nch - 1);  // lanes past the row's end reload its last chunk
 #pragma unroll
-  for (int r = 0; r < DEC_RW; ++r)
+      for (int r = 0; r < RW; ++r) {
+        load_chunk<BITS>(gw + r * rbytes, c, W.gd[q][r]);
+        load_chunk<BITS>(uw + r * rbytes, c, W.ud[q][r]);
+        W.gsc[q][r] = L.gate.s[gso + r * ng + (c >> 1)];
+        W.gbi[q][r] = L.gate.b[gso + r * ng + (c >> 1)];
+        W.usc[q][r] = L.up.s[uso + r * ng + (c >> 1)];
+        W.ubi[q][r] = L.up.b[uso + r * ng + (c >> 1)];
+      }
+    }
+  };
+  auto compute_item = [&](int item, const WStage& W) {
+    const int u = item / A.wgs_per_expert;
+    const int rb = item - u * A.wgs_per_expert;
+    const int p0 = s_ustart[u];
+    const int na = min(s_ustart[u + 1] - p0, NT);
+    const int ib = rb * (4 * RW) + wave * RW;
+    int asg[NT], tok[NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) ag[r][j] = au[r][j] = 0.f;
-
-  for (int c = lane; c < nch; c += 64) {
-    uint32_t gd[DEC_RW][4], ud[DEC_RW][4];
-    uint16_t gsc[DEC_RW], gbi[DEC_RW], usc[DEC_RW], ubi[DEC_RW];
+    for (int j = 0; j < NT; ++j) {
+      asg[j] = j < na ? s_perm[p0 + j] : 0;
+      tok[j] = asg[j] / K;
+    }
+    float ag[RW][NT], au[RW][NT];
 #pragma unroll
-    for (int r = 0; r < DEC_RW; ++r) {
-      load_chunk<BITS>(gw + r * rbytes, c, gd[r]);
-      load_chunk<BITS>(uw + r * rbytes, c, ud[r]);
-      gsc[r] = L.gate.s[gso + r * ng + (c >> 1)];
-      gbi[r] = L.gate.b[gso + r * ng + (c >> 1)];
-      usc[r] = L.up.s[uso + r * ng + (c >> 1)];
-      ubi[r] = L.up.b[uso + r * ng + (c >> 1)];
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) ag[r][j] = au[r][j] = 0.f;
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+      const int c = lane + 64 * q;
+      if (c < nch) {
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          uint32_t cg[16], cu[16];
+          unpack_chunk<BITS, false>(W.gd[q][r], cg);
+          unpack_chunk<BITS, false>(W.ud[q][r], cu);
+          const float sg = scale_to_f32<BF16>(W.gsc[q][r]) * TWO24, bg = scale_to_f32<BF16>(W.gbi[q][r]);
+          const float su = scale_to_f32<BF16>(W.usc[q][r]) * TWO24, bu = scale_to_f32<BF16>(W.ubi[q][r]);
+#pragma unroll
+          for (int j = 0; j < NT; ++j) {
+            if (j < na) {
+              uint32_t xv[16];
+              load16(xs + ((size_t)tok[j] * nch + c) * 16, xv);
+              const float xsm = xsum[tok[j] * nch + c];
+              ag[r][j] += sg * chunk_dot(cg, xv) + bg * xsm;
+              au[r][j] += su * chunk_dot(cu, xv) + bu * xsm;
+            }
+          }
+        }
+      }
     }
 #pragma unroll
-    for (int r = 0; r < DEC_RW; ++r) {
-      uint32_t cg[16], cu[16];
-      unpack_chunk<BITS, false>(gd[r], cg);
-      unpack_chunk<BITS, false>(ud[r], cu);
-      const float sg = scale_to_f32<BF16>(gsc[r]) * TWO24, bg = scale_to_f32<BF16>(gbi[r]);
-      const float su = scale_to_f32<BF16>(usc[r]) * TWO24, bu = scale_to_f32<BF16>(ubi[r]);
+    for (int r = 0; r < RW; ++r) {
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         if (j < na) {
-          uint32_t xv[16];
-          load16(xs + ((size_t)tok[j] * nch + c) * 16, xv);
-          const float xsm = xsum[tok[j] * nch + c];
-          ag[r][j] += sg * chunk_dot(cg, xv) + bg * xsm;
-          au[r][j] += su * chunk_dot(cu, xv) + bu * xsm;
+          const float g = wave_sum_dpp(ag[r][j]);
+          const float uu = wave_sum_dpp(au[r][j]);
+          if (lane == 0) {
+            const int i = ib + r;
+            const float a = activate<ACT>(g, uu);
+            const _Float16 hi = (_Float16)a;
+            const _Float16 lo = (_Float16)(a - (float)hi);
+            const size_t o = (size_t)asg[j] * I + (i & ~31) + pairpos<BITS>(i & 31);
+            A.act[o] = __builtin_bit_cast(uint16_t, hi);
+            A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
+          }
         }
       }
     }
+    KMOE_MARK(0, 4);
+  };
+  WStage W0, W1;
+  const int step = gridDim.x;
+  int item = blockIdx.x;
+  if (item < nitems) load_item(item, W0);
+  for (; item < nitems; item += 2 * step) {
+    if (item + step < nitems) load_item(item + step, W1);
+    compute_item(item, W0);
+    if (item + step >= nitems) break;
+    if (item + 2 * step < nitems) load_item(item + 2 * step, W0);
+    compute_item(item + step, W1);
   }
-#pragma unroll
-  for (int r = 0; r < DEC_RW; ++r) {
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      if (j < na) {
-        const float g = wave_sum_dpp(ag[r][j]);
-        const float uu = wave_sum_dpp(au[r][j]);
-        if (lane == 0) {
-          const int i = ib + r;
-          const float a = activate<ACT>(g, uu);
-          const _Float16 hi = (_Float16)a;
-          const _Float16 lo = (_Float16)(a - (float)hi);
-          const size_t o = (size_t)asg[j] * I + (i & ~31) + pairpos<BITS>(i & 31);
-          A.act[o] = __builtin_bit_cast(uint16_t, hi);
-          A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
-        }
-      }
-    }
-  }
-  KMOE_MARK(0, 4);
-  }  // item loop
   KMOE_MARK(0, 5);
 }
 
@@ -701,7 +730,7 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   A.scalars = w.scalars;
   A.act = w.act;
   A.act_plane = (size_t)T * K * L.I;
-  A.wgs_per_expert = L.I / (4 * DEC_RW);
+  A.wgs_per_expert = L.I / (4 * (NT == 1 ? DEC_RW : stage1_rw(NT)));
   // at most two workgroups per CU: every workgroup repeats the routing and x staging, so
   // the grid stays resident and loops over the (expert, row block) items instead
   const int grid1 = min(min(T * K, L.E) * A.wgs_per_expert, 2 * cu_count());
@@ -716,8 +745,12 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
       err = d.logits ? launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 2, true>, grid1, 0, s, A)
                      : launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 2, false>, grid1, 0, s, A);
   } else {
-    err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, true>, grid1, lds1, s, A)
-                   : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, false>, grid1, lds1, s, A);
+    if (nch <= 64)
+      err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, 1, true>, grid1, lds1, s, A)
+                     : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, 1, false>, grid1, lds1, s, A);
+    else
+      err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, 2, true>, grid1, lds1, s, A)
+                     : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, 2, false>, grid1, lds1, s, A);
   }
   if (err != hipSuccess) return err;
   const int l2 = lpa_log2_for(L.I);
