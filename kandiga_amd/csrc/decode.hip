@@ -115,8 +115,9 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   __shared__ int32_t s_e[DEC_MAX_ASSIGN];
   __shared__ float s_w[DEC_MAX_ASSIGN];
   __shared__ int32_t s_perm[DEC_MAX_ASSIGN];
-  __shared__ int32_t s_unique[DEC_MAX_ASSIGN];
-  __shared__ int32_t s_ustart[DEC_MAX_ASSIGN + 1];
+  __shared__ int32_t s_ptok[DEC_MAX_ASSIGN];
+  __shared__ int32_t s_slot_e[DEC_MAX_ASSIGN];
+  __shared__ int32_t s_slot_p[DEC_MAX_ASSIGN + 1];
   __shared__ int32_t s_tmp[4];
 
   const LayerArgs& L = A.L;
@@ -169,9 +170,11 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   }
   __syncthreads();
   KMOE_MARK(0, 2);
-  // stable grouping of the valid assignments by expert: s_perm lists them by (expert, id),
-  // s_unique / s_ustart give each distinct expert and the start of its run
-  int nvalid, nu;
+  // Stable grouping of the valid assignments by expert: s_perm lists them by (expert, id) and
+  // s_ptok gives each sorted position's token.  Each expert's run is cut into slots of at most
+  // NT assignments (given indices may repeat an expert within a token, so a run can exceed T):
+  // slot s covers positions s_slot_p[s] .. s_slot_p[s+1]-1, all of expert s_slot_e[s].
+  int nvalid, nu, nsl;
   if (TK <= 64) {
     if (wave == 0) {  // one wave, lane a holds assignment a: ranks by a radix pass of ballots
       const int e = lane < TK ? s_e[lane] : -1;
@@ -188,31 +191,41 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
         less += one ? __popcll(eq & ~ones) : 0;
         eq &= one ? ones : ~ones;
       }
-      const int r = less + __popcll(eq & below);
-      const bool first = valid && (eq & below) == 0;
-      uint64_t eqf = __ballot(first);
-      int ur = 0;
+      const int within = __popcll(eq & below);  // rank inside the expert's run
+      const int r = less + within;
+      const bool first = valid && within == 0;
+      const bool sfirst = valid && within % NT == 0;
+      // slot-opening lanes of smaller experts, by the same radix pass
+      uint64_t eqs = __ballot(sfirst);
+      int sless = 0;
       for (int bit = nbits - 1; bit >= 0; --bit) {
         const bool one = (e >> bit) & 1;
-        const uint64_t ones = __ballot(first && one);
-        ur += one ? __popcll(eqf & ~ones) : 0;
-        eqf &= one ? ones : ~ones;
+        const uint64_t ones = __ballot(sfirst && one);
+        sless += one ? __popcll(eqs & ~ones) : 0;
+        eqs &= one ? ones : ~ones;
       }
-      if (valid) s_perm[r] = lane;
-      if (first) {
-        s_unique[ur] = e;
-        s_ustart[ur] = r;
+      if (valid) {
+        s_perm[r] = lane;
+        s_ptok[r] = lane / K;
+      }
+      if (sfirst) {
+        const int sl = sless + within / NT;
+        s_slot_e[sl] = e;
+        s_slot_p[sl] = r;
       }
       const int nv = __popcll(__ballot(valid)), nf = __popcll(__ballot(first));
+      const int ns = __popcll(__ballot(sfirst));
       if (lane == 0) {
-        s_ustart[nf] = nv;
+        s_slot_p[ns] = nv;
         s_tmp[0] = nv;
         s_tmp[1] = nf;
+        s_tmp[2] = ns;
       }
     }
     __syncthreads();
     nvalid = s_tmp[0];
     nu = s_tmp[1];
+    nsl = s_tmp[2];
   } else {
     const int my_e = tid < TK ? s_e[tid] : -1;
     if (my_e >= 0) {
@@ -223,20 +236,27 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
         r += (eb >= 0) & ((eb * DEC_MAX_ASSIGN + b) < key);
       }
       s_perm[r] = tid;
+      s_ptok[r] = tid / K;
     }
     block_prefix_count(my_e >= 0, s_tmp, &nvalid);  // its barriers also order the s_perm writes
-    int pe = -1;
-    bool first = false;
+    int pe = -1, within = 0;
     if (tid < nvalid) {
       pe = s_e[s_perm[tid]];
-      first = tid == 0 || s_e[s_perm[tid - 1]] != pe;
+      int rs = 0;  // start of this expert's run: valid assignments of smaller experts
+      for (int b = 0; b < TK; ++b) {
+        const int eb = s_e[b];
+        rs += (eb >= 0) & (eb < pe);
+      }
+      within = tid - rs;
     }
-    const int ur = block_prefix_count(first, s_tmp, &nu);
-    if (first) {
-      s_unique[ur] = pe;
-      s_ustart[ur] = tid;
+    block_prefix_count(tid < nvalid && within == 0, s_tmp, &nu);
+    const bool sfirst = tid < nvalid && within % NT == 0;
+    const int sl = block_prefix_count(sfirst, s_tmp, &nsl);
+    if (sfirst) {
+      s_slot_e[sl] = pe;
+      s_slot_p[sl] = tid;
     }
-    if (tid == 0) s_ustart[nu] = nvalid;
+    if (tid == 0) s_slot_p[nsl] = nvalid;
     __syncthreads();
   }
   if (lead && tid == 0) {
@@ -245,97 +265,121 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   }
 
   KMOE_MARK(0, 3);
-  // (expert slot, block of 4*RW rows) items, grid-strided over the workgroups.  The weights of
-  // the next item are loaded while the current one is computed (two register stages,
-  // unrolled by two so no stage is copied while its loads are in flight).
+  // (slot, block of 4*RW rows) items, grid-strided over the workgroups.  The weights of the
+  // next item are loaded while the current one is computed (two register stages, unrolled by
+  // two so no stage is copied while its loads are in flight).  Weights come through buffer
+  // resources made per expert: the row offset is a scalar and the lane's chunk offset a
+  // constant, so no per-load address arithmetic runs on the vector ALU.
   constexpr int RW = stage1_rw(NT);
-  const int nitems = nu * A.wgs_per_expert;
-  const size_t rbytes = (size_t)H * BITS / 8;
+  constexpr int V = 2 * RW;  // reduced values per token: gate then up, of RW rows
+  const int wpe = A.wgs_per_expert;
+  const int nitems = nsl * wpe;
+  const uint32_t rbytes = (uint32_t)H * BITS / 8;
   const int ng = H / GROUP;
+  const uint32_t wbytes = (uint32_t)I * rbytes, sbytes = (uint32_t)I * ng * 2;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t cvo[CPL], svo[CPL];
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) {
+    const int c = min(lane + 64 * q, nch - 1);  // lanes past the row's end reload its last chunk
+    cvo[q] = (uint32_t)c * Bits<BITS>::chunk_bytes;
+    svo[q] = (uint32_t)(c >> 1) * 2u;
+  }
   struct WStage {
     uint32_t gd[CPL][RW][4], ud[CPL][RW][4];
     uint16_t gsc[CPL][RW], gbi[CPL][RW], usc[CPL][RW], ubi[CPL][RW];
   };
   auto load_item = [&](int item, WStage& W) {
-    const int u = item / A.wgs_per_expert;
-    const int rb = item - u * A.wgs_per_expert;
-    const int e = s_unique[u];
-    const int ib = rb * (4 * RW) + wave * RW;
-    const uint8_t* gw = L.gate.w + (size_t)e * L.gate.w_stride + (size_t)ib * rbytes;
-    const uint8_t* uw = L.up.w + (size_t)e * L.up.w_stride + (size_t)ib * rbytes;
-    const size_t gso = (size_t)e * L.gate.s_stride + (size_t)ib * ng;
-    const size_t uso = (size_t)e * L.up.s_stride + (size_t)ib * ng;
+    const int sl = item / wpe;
+    const int rb = item - sl * wpe;
+    const int e = __builtin_amdgcn_readfirstlane(s_slot_e[sl]);
+    const int ib = rb * (4 * RW) + wv * RW;
+    const auto gw = make_rsrc(L.gate.w + (size_t)e * L.gate.w_stride, wbytes);
+    const auto uw = make_rsrc(L.up.w + (size_t)e * L.up.w_stride, wbytes);
+    const auto gs = make_rsrc(L.gate.s + (size_t)e * L.gate.s_stride, sbytes);
+    const auto gb = make_rsrc(L.gate.b + (size_t)e * L.gate.s_stride, sbytes);
+    const auto us = make_rsrc(L.up.s + (size_t)e * L.up.s_stride, sbytes);
+    const auto ub = make_rsrc(L.up.b + (size_t)e * L.up.s_stride, sbytes);
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
-      const int c = min(lane + 64 * q, nch - 1);  // lanes past the row's end reload its last chunk
 #pragma unroll
       for (int r = 0; r < RW; ++r) {
-        load_chunk<BITS>(gw + r * rbytes, c, W.gd[q][r]);
-        load_chunk<BITS>(uw + r * rbytes, c, W.ud[q][r]);
-        W.gsc[q][r] = L.gate.s[gso + r * ng + (c >> 1)];
-        W.gbi[q][r] = L.gate.b[gso + r * ng + (c >> 1)];
-        W.usc[q][r] = L.up.s[uso + r * ng + (c >> 1)];
-        W.ubi[q][r] = L.up.b[uso + r * ng + (c >> 1)];
+        const uint32_t wo = (uint32_t)(ib + r) * rbytes, so = (uint32_t)(ib + r) * ng * 2u;
+        buf_chunk<BITS>(gw, cvo[q], wo, W.gd[q][r]);
+        buf_chunk<BITS>(uw, cvo[q], wo, W.ud[q][r]);
+        W.gsc[q][r] = buf_u16(gs, svo[q], so);
+        W.gbi[q][r] = buf_u16(gb, svo[q], so);
+        W.usc[q][r] = buf_u16(us, svo[q], so);
+        W.ubi[q][r] = buf_u16(ub, svo[q], so);
       }
     }
   };
   auto compute_item = [&](int item, const WStage& W) {
-    const int u = item / A.wgs_per_expert;
-    const int rb = item - u * A.wgs_per_expert;
-    const int p0 = s_ustart[u];
-    const int na = min(s_ustart[u + 1] - p0, NT);
-    const int ib = rb * (4 * RW) + wave * RW;
-    int asg[NT], tok[NT];
+    const int sl = item / wpe;
+    const int rb = item - sl * wpe;
+    const int p0 = __builtin_amdgcn_readfirstlane(s_slot_p[sl]);
+    const int na = __builtin_amdgcn_readfirstlane(s_slot_p[sl + 1]) - p0;  // 1..NT
+    const int ib = rb * (4 * RW) + wv * RW;
+    // act column of the row this lane stores after the reduction (row r sits in lane group r)
+    int col = 0;
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      asg[j] = j < na ? s_perm[p0 + j] : 0;
-      tok[j] = asg[j] / K;
+    for (int r = 0; r < RW; ++r) {
+      const int i = ib + r;
+      const int cr = (i & ~31) + pairpos<BITS>(i & 31);
+      col = (lane >> (V == 8 ? 3 : 4)) == r ? cr : col;
     }
-    float ag[RW][NT], au[RW][NT];
-#pragma unroll
-    for (int r = 0; r < RW; ++r)
-#pragma unroll
-      for (int j = 0; j < NT; ++j) ag[r][j] = au[r][j] = 0.f;
+    // acc[j][gu * RW + r]: token j's gate (gu = 0) or up (gu = 1) partial of row r
+    float acc[NT][V];
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
       const int c = lane + 64 * q;
-      if (c < nch) {
+      const int cc = min(c, nch - 1);
+      const bool cv = c < nch;
 #pragma unroll
-        for (int r = 0; r < RW; ++r) {
-          uint32_t cg[16], cu[16];
-          unpack_chunk<BITS, false>(W.gd[q][r], cg);
-          unpack_chunk<BITS, false>(W.ud[q][r], cu);
-          const float sg = scale_to_f32<BF16>(W.gsc[q][r]) * TWO24, bg = scale_to_f32<BF16>(W.gbi[q][r]);
-          const float su = scale_to_f32<BF16>(W.usc[q][r]) * TWO24, bu = scale_to_f32<BF16>(W.ubi[q][r]);
+      for (int r = 0; r < RW; ++r) {
+        uint32_t cg[16], cu[16];
+        unpack_chunk<BITS, false>(W.gd[q][r], cg);
+        unpack_chunk<BITS, false>(W.ud[q][r], cu);
+        const float sg = scale_to_f32<BF16>(W.gsc[q][r]) * TWO24, bg = scale_to_f32<BF16>(W.gbi[q][r]);
+        const float su = scale_to_f32<BF16>(W.usc[q][r]) * TWO24, bu = scale_to_f32<BF16>(W.ubi[q][r]);
 #pragma unroll
-          for (int j = 0; j < NT; ++j) {
-            if (j < na) {
-              uint32_t xv[16];
-              load16(xs + ((size_t)tok[j] * nch + c) * 16, xv);
-              const float xsm = xsum[tok[j] * nch + c];
-              ag[r][j] += sg * chunk_dot(cg, xv) + bg * xsm;
-              au[r][j] += su * chunk_dot(cu, xv) + bu * xsm;
+        for (int j = 0; j < NT; ++j) {
+          if (j < na) {
+            const int t = __builtin_amdgcn_readfirstlane(s_ptok[p0 + j]);
+            uint32_t xv[16];
+            load16(xs + ((size_t)t * nch + cc) * 16, xv);
+            const float xsm = xsum[t * nch + cc];
+            float dg = sg * chunk_dot(cg, xv) + bg * xsm;
+            float du = su * chunk_dot(cu, xv) + bu * xsm;
+            if (!cv) dg = du = 0.f;
+            if (q == 0) {
+              acc[j][r] = dg;
+              acc[j][RW + r] = du;
+            } else {
+              acc[j][r] += dg;
+              acc[j][RW + r] += du;
             }
           }
         }
       }
     }
+    // lane groups 0..RW-1 hold the gate totals of rows 0..RW-1, groups RW..2RW-1 the up totals:
+    // one swap of the wave halves puts each row's up total beside its gate total
+    const bool store_lane = lane < 32 && (lane & (64 / V - 1)) == 0;
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        if (j < na) {
-          const float g = wave_sum_dpp(ag[r][j]);
-          const float uu = wave_sum_dpp(au[r][j]);
-          if (lane == 0) {
-            const int i = ib + r;
-            const float a = activate<ACT>(g, uu);
-            const _Float16 hi = (_Float16)a;
-            const _Float16 lo = (_Float16)(a - (float)hi);
-            const size_t o = (size_t)asg[j] * I + (i & ~31) + pairpos<BITS>(i & 31);
-            A.act[o] = __builtin_bit_cast(uint16_t, hi);
-            A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
-          }
+    for (int j = 0; j < NT; ++j) {
+      if (j < na) {
+        const float g = wave_sum_multi<V>(acc[j]);
+        const float u = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(g), __float_as_uint(g),
+                                                                         false, false)[1]);
+        const int asg = __builtin_amdgcn_readfirstlane(s_perm[p0 + j]);
+        if (store_lane) {
+          const float a = activate<ACT>(g, u);
+          const _Float16 hi = (_Float16)a;
+          const _Float16 lo = (_Float16)(a - (float)hi);
+          const size_t o = (size_t)asg * I + col;
+          A.act[o] = __builtin_bit_cast(uint16_t, hi);
+          A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
         }
       }
     }
@@ -432,8 +476,12 @@ __global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) 
   KMOE_MARK(0, 3);
 
   const int nitems = nu * A.wgs_per_expert;
-  const size_t rbytes = (size_t)H * BITS / 8;
+  constexpr int V = 2 * DEC_RW;  // reduced values: gate then up, of DEC_RW rows
+  const uint32_t rbytes = (uint32_t)H * BITS / 8;
   const int ng = H / GROUP;
+  const uint32_t wbytes = (uint32_t)I * rbytes, sbytes = (uint32_t)I * ng * 2;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const bool store_lane = lane < 32 && (lane & (64 / V - 1)) == 0;
   for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
     const int u = item / A.wgs_per_expert;
     const int rb = item - u * A.wgs_per_expert;
@@ -441,31 +489,43 @@ __global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) 
     for (int q = 0; q < u; ++q) fm &= fm - 1ull;
     const int e = __builtin_amdgcn_readlane(my, (int)__builtin_ctzll(fm));
     const uint64_t amask = __ballot(my == e);
-    const int ib = rb * (4 * DEC_RW) + wave * DEC_RW;
-    const uint8_t* gw = L.gate.w + (size_t)e * L.gate.w_stride + (size_t)ib * rbytes;
-    const uint8_t* uw = L.up.w + (size_t)e * L.up.w_stride + (size_t)ib * rbytes;
-    const size_t gso = (size_t)e * L.gate.s_stride + (size_t)ib * ng;
-    const size_t uso = (size_t)e * L.up.s_stride + (size_t)ib * ng;
+    const int ib = rb * (4 * DEC_RW) + wv * DEC_RW;
+    // buffer resources of this expert: scalar row offsets, constant per-lane chunk offsets
+    const auto gw = make_rsrc(L.gate.w + (size_t)e * L.gate.w_stride, wbytes);
+    const auto uw = make_rsrc(L.up.w + (size_t)e * L.up.w_stride, wbytes);
+    const auto gs = make_rsrc(L.gate.s + (size_t)e * L.gate.s_stride, sbytes);
+    const auto gb = make_rsrc(L.gate.b + (size_t)e * L.gate.s_stride, sbytes);
+    const auto us = make_rsrc(L.up.s + (size_t)e * L.up.s_stride, sbytes);
+    const auto ub = make_rsrc(L.up.b + (size_t)e * L.up.s_stride, sbytes);
     uint32_t gd[CPL][DEC_RW][4], ud[CPL][DEC_RW][4];
     uint16_t gsc[CPL][DEC_RW], gbi[CPL][DEC_RW], usc[CPL][DEC_RW], ubi[CPL][DEC_RW];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int c = lane + 64 * j;
-      if (c < nch) {
+      const int c = min(lane + 64 * j, nch - 1);  // lanes past the row's end reload its last chunk
+      const uint32_t cvo = (uint32_t)c * Bits<BITS>::chunk_bytes, svo = (uint32_t)(c >> 1) * 2u;
 #pragma unroll
-        for (int r = 0; r < DEC_RW; ++r) {
-          load_chunk<BITS>(gw + r * rbytes, c, gd[j][r]);
-          load_chunk<BITS>(uw + r * rbytes, c, ud[j][r]);
-          gsc[j][r] = L.gate.s[gso + r * ng + (c >> 1)];
-          gbi[j][r] = L.gate.b[gso + r * ng + (c >> 1)];
-          usc[j][r] = L.up.s[uso + r * ng + (c >> 1)];
-          ubi[j][r] = L.up.b[uso + r * ng + (c >> 1)];
-        }
+      for (int r = 0; r < DEC_RW; ++r) {
+        const uint32_t wo = (uint32_t)(ib + r) * rbytes, so = (uint32_t)(ib + r) * ng * 2u;
+        buf_chunk<BITS>(gw, cvo, wo, gd[j][r]);
+        buf_chunk<BITS>(uw, cvo, wo, ud[j][r]);
+        gsc[j][r] = buf_u16(gs, svo, so);
+        gbi[j][r] = buf_u16(gb, svo, so);
+        usc[j][r] = buf_u16(us, svo, so);
+        ubi[j][r] = buf_u16(ub, svo, so);
       }
     }
-    float ag[DEC_RW], au[DEC_RW];
+    // act column of the row this lane stores after the reduction (row r sits in lane group r)
+    int col = 0;
 #pragma unroll
-    for (int r = 0; r < DEC_RW; ++r) ag[r] = au[r] = 0.f;
+    for (int r = 0; r < DEC_RW; ++r) {
+      const int i = ib + r;
+      const int cr = (i & ~31) + pairpos<BITS>(i & 31);
+      col = (lane >> (V == 8 ? 3 : 4)) == r ? cr : col;
+    }
+    // acc[gu * DEC_RW + r]: gate (gu = 0) or up (gu = 1) partial of row r
+    float acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = 0.f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       if (lane + 64 * j < nch) {
@@ -474,26 +534,25 @@ __global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) 
           uint32_t cg[16], cu[16];
           unpack_chunk<BITS, false>(gd[j][r], cg);
           unpack_chunk<BITS, false>(ud[j][r], cu);
-          ag[r] += scale_to_f32<BF16>(gsc[j][r]) * TWO24 * chunk_dot(cg, xp[j]) + scale_to_f32<BF16>(gbi[j][r]) * xs[j];
-          au[r] += scale_to_f32<BF16>(usc[j][r]) * TWO24 * chunk_dot(cu, xp[j]) + scale_to_f32<BF16>(ubi[j][r]) * xs[j];
+          acc[r] += scale_to_f32<BF16>(gsc[j][r]) * TWO24 * chunk_dot(cg, xp[j]) + scale_to_f32<BF16>(gbi[j][r]) * xs[j];
+          acc[DEC_RW + r] +=
+              scale_to_f32<BF16>(usc[j][r]) * TWO24 * chunk_dot(cu, xp[j]) + scale_to_f32<BF16>(ubi[j][r]) * xs[j];
         }
       }
     }
-#pragma unroll
-    for (int r = 0; r < DEC_RW; ++r) {
-      const float g = wave_sum_dpp(ag[r]);
-      const float uu = wave_sum_dpp(au[r]);
-      if (lane == 0) {
-        const int i = ib + r;
-        const float a = activate<ACT>(g, uu);
-        const _Float16 hi = (_Float16)a;
-        const _Float16 lo = (_Float16)(a - (float)hi);
-        const size_t col = (size_t)(i & ~31) + pairpos<BITS>(i & 31);
-        for (uint64_t m = amask; m; m &= m - 1ull) {
-          const size_t o = (size_t)__builtin_ctzll(m) * I + col;
-          A.act[o] = __builtin_bit_cast(uint16_t, hi);
-          A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
-        }
+    // lane groups 0..DEC_RW-1 hold the gate totals, DEC_RW..2*DEC_RW-1 the up totals: one swap
+    // of the wave halves puts each row's up total beside its gate total
+    const float g = wave_sum_multi<V>(acc);
+    const float uu =
+        __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(g), __float_as_uint(g), false, false)[1]);
+    if (store_lane) {
+      const float a = activate<ACT>(g, uu);
+      const _Float16 hi = (_Float16)a;
+      const _Float16 lo = (_Float16)(a - (float)hi);
+      for (uint64_t m = amask; m; m &= m - 1ull) {  // every assignment of this expert (repeats are rare)
+        const size_t o = (size_t)__builtin_ctzll(m) * I + col;
+        A.act[o] = __builtin_bit_cast(uint16_t, hi);
+        A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
       }
     }
     KMOE_MARK(0, 4);

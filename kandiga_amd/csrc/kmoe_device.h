@@ -250,6 +250,73 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
 }
 
+// Sums V per-lane values (V = 4 or 8) over the wave in one pass.  Each step halves the values a
+// lane carries: v_permlane32_swap / v_permlane16_swap (gfx950) hand one value of every pair to
+// the partner half, so each half sums a different value, then DPP finishes inside 16-lane rows.
+// The total of value v ends in every lane of lane group v: lanes 8v..8v+7 for V = 8 and
+// 16v..16v+15 for V = 4.  About 3V/2 + 6 instructions, against 7V for V separate reductions.
+template <int V>
+__device__ __forceinline__ float wave_sum_multi(const float (&v)[V]) {
+  static_assert(V == 4 || V == 8, "V must be 4 or 8");
+  float w[V / 2];
+#pragma unroll
+  for (int i = 0; i < V / 2; ++i) {
+    // lanes 0-31 end with v[i] of lanes l and l+32, lanes 32-63 with v[i + V/2] of l-32 and l
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + V / 2]), false,
+                                                    false);
+    w[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  float x[V / 4];
+#pragma unroll
+  for (int i = 0; i < V / 4; ++i) {
+    // rows 0 and 2 end with w[i] of rows (0,1) and (2,3); rows 1 and 3 with w[i + V/4]
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[i]), __float_as_uint(w[i + V / 4]), false,
+                                                    false);
+    x[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  float y;
+  if constexpr (V == 8) {
+    // lanes with bit 3 clear keep x[0] and lanes with it set keep x[1], each adding lane l ^ 8's
+    const bool b3 = (__lane_id() & 8) != 0;
+    const float keep = b3 ? x[1] : x[0], give = b3 ? x[0] : x[1];
+    y = keep + dpp_f32<0x128>(give);  // row_ror:8
+    y += dpp_f32<0xB1>(y);            // quad_perm [1,0,3,2]
+    y += dpp_f32<0x4E>(y);            // quad_perm [2,3,0,1]
+    y += dpp_f32<0x141>(y);           // row_half_mirror
+  } else {
+    y = x[0];
+    y += dpp_f32<0x128>(y);
+    y += dpp_f32<0x141>(y);
+    y += dpp_f32<0xB1>(y);
+    y += dpp_f32<0x4E>(y);
+  }
+  return y;
+}
+
+// Buffer resource over `bytes` bytes at `base` (raw, untyped dword access; loads past the end
+// return zero).  Built in scalar registers when its arguments are uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+constexpr int BUF_NT = 2;  // cache-policy bit of a buffer load: non-temporal (streamed once)
+
+// One chunk of packed codes through a buffer resource: byte offset voff (per lane) + soff (uniform).
+template <int BITS>
+__device__ __forceinline__ void buf_chunk(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint32_t (&d)[4]) {
+  if constexpr (BITS == 3) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, BUF_NT);
+    d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = 0;
+  } else {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, BUF_NT);
+    d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+  }
+}
+
+__device__ __forceinline__ uint16_t buf_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
 // Orderable key of a router logit: larger logit -> larger key, +0 == -0, NaN below all.
 __device__ __forceinline__ uint32_t logit_key(float v) {
   if (v != v) return 0u;

@@ -104,6 +104,29 @@ def test_switch_mlp_small(device, name, T):
     assert_close(to_np(y), ref, what=f"{name} T={T} switch_mlp")
 
 
+@pytest.mark.parametrize("K,T,pattern", [(4, 1, "same"), (4, 3, "same"), (4, 8, "same"), (4, 8, "random"),
+                                          (4, 12, "same"), (16, 5, "random"), (16, 8, "same"), (16, 8, "random")])
+def test_switch_mlp_repeated_experts(device, K, T, pattern):
+    """Given indices may repeat an expert within a token (the reference computes every (t, k)
+    independently, kandiga_cpu_expert.m:471-552): one expert's run then exceeds the token count.
+    K=16 puts up to 128 assignments through the block-wide grouping of the decode path."""
+    from kandiga_amd.moe import QuantizedSwitchGLU
+
+    shape = synth.LayerShape(256, 128, 32, K, 3)
+    layer, ex = _experts(shape, 23, device)
+    x, _ = synth.make_inputs(shape, T, 24)
+    rng = np.random.default_rng(25 + T)
+    if pattern == "same":
+        idx = np.full((T, K), 5, dtype=np.int32)
+        idx[:, -1] = 7
+    else:
+        idx = rng.integers(0, 6, size=(T, K)).astype(np.int32)  # few experts, many repeats
+    y = QuantizedSwitchGLU(ex)(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device))
+    assert ex.device_status() == 0
+    ref = O.switch_mlp(layer, x, idx, shape.bits)
+    assert_close(to_np(y), ref, what=f"K={K} T={T} {pattern} switch_mlp")
+
+
 @pytest.mark.parametrize("name", sorted(SMALL))
 @pytest.mark.parametrize("T", [1, 2, 5, 8, 9, 64, 700])
 def test_forward_small(device, name, T):
