@@ -130,19 +130,41 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   const bool lead = blockIdx.x == 0;
   KMOE_MARK(0, 0);
 
-  // x of every token, pair order, with per-chunk sums.  Each thread's first chunk is loaded
-  // before the routing code so its latency overlaps the logits loads.
+  // x of every token, pair order, with per-chunk sums.  Each thread's first two chunks are
+  // loaded before the routing code so their latency overlaps the logits loads.
   const int ntask = T * nch;
-  uint32_t xpre[16];
-  if (tid < ntask) load16(A.x + (size_t)(tid / nch) * H + (size_t)(tid % nch) * CHUNK, xpre);
+  uint32_t xpre[2][16];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int task = tid + 256 * j;
+    if (task < ntask) load16(A.x + (size_t)(task / nch) * H + (size_t)(task % nch) * CHUNK, xpre[j]);
+  }
 
   // routing, or the given indices (out-of-range experts are dropped and flagged)
   if constexpr (ROUTE) {
-    for (int t = wave; t < T; t += 4) {
-      const float* row = A.logits + (size_t)t * E;
-      int32_t* io = lead && A.idx_out ? A.idx_out + t * K : nullptr;
-      float* wo = lead && A.w_out ? A.w_out + t * K : nullptr;
-      KMOE_TOPK_DISPATCH(E, (wave_topk<EPL_>(row, E, K, io, wo, s_e + t * K, s_w + t * K)));
+    auto publish = [&](int t, int e, float w) {
+      if (lane < K) {
+        s_e[t * K + lane] = e;
+        s_w[t * K + lane] = w;
+        if (lead && A.idx_out) A.idx_out[t * K + lane] = e;
+        if (lead && A.w_out) A.w_out[t * K + lane] = w;
+      }
+    };
+    if (T > 4) {
+      // tokens wave and wave + 4 as two interleaved chains; past the end the second repeats the
+      // first and its result is dropped
+      const int t1 = wave + 4 < T ? wave + 4 : wave;
+      const float* const rows[2] = {A.logits + (size_t)wave * E, A.logits + (size_t)t1 * E};
+      int se[2];
+      float sw[2];
+      KMOE_TOPK_DISPATCH(E, (wave_topk_rows<EPL_, 2>(rows, E, K, se, sw)));
+      publish(wave, se[0], sw[0]);
+      if (wave + 4 < T) publish(wave + 4, se[1], sw[1]);
+    } else if (wave < T) {
+      int se;
+      float sw;
+      KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(A.logits + (size_t)wave * E, E, K, se, sw)));
+      publish(wave, se, sw);
     }
   } else {
     for (int a = tid; a < TK; a += 256) {
@@ -155,7 +177,10 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
     uint32_t nat[16], pr[16];
     if (task == tid) {
 #pragma unroll
-      for (int q = 0; q < 16; ++q) nat[q] = xpre[q];
+      for (int q = 0; q < 16; ++q) nat[q] = xpre[0][q];
+    } else if (task == tid + 256) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) nat[q] = xpre[1][q];
     } else {
       load16(A.x + (size_t)(task / nch) * H + (size_t)(task % nch) * CHUNK, nat);
     }
@@ -560,7 +585,6 @@ __global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) 
   KMOE_MARK(0, 5);
 }
 
-constexpr int S2_ROWS = 8;  // output rows per stage-2 workgroup
 
 // Stage 2.  Lane (g, c) of a wave works on assignment g of its unit and 32-wide chunk c of the
 // intermediate dimension, for RPW consecutive output rows: each act chunk is loaded once per
@@ -568,7 +592,7 @@ constexpr int S2_ROWS = 8;  // output rows per stage-2 workgroup
 // subset of the workgroup's S2_ROWS rows); the four waves take units round-robin, UF at a
 // time with all their loads in flight.  Per-assignment row results go to LDS and the combine
 // sums them in k order (moe_block.metal:515-539), so the result does not depend on timing.
-template <int BITS, bool BF16, int RPW, int UF, bool COMBINE>
+template <int BITS, bool BF16, int S2_ROWS, int RPW, int UF, bool COMBINE>
 __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int T, int K,
                                                          const int32_t* __restrict__ idx,
                                                          const float* __restrict__ wts,
@@ -813,16 +837,19 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   }
   if (err != hipSuccess) return err;
   const int l2 = lpa_log2_for(L.I);
-  constexpr int RPW = NT == 1 ? 4 : 8;
+  // output rows per workgroup and per unit: the single-token layer has few units, so a unit's
+  // rows are split between waves; more tokens give enough units for 4-row units on a doubled grid
+  constexpr int S2_ROWS = NT == 1 ? 8 : 4;
+  constexpr int RPW = 4;
   constexpr int UF = 2;
   const int32_t* idx = d.idx_in ? d.idx_in : d.idx_out;
   const dim3 grid2(L.H / S2_ROWS);
   if (d.combine) {
-    KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, RPW, UF, true>), grid2, dim3(256), 0, s, L, T,
+    KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, S2_ROWS, RPW, UF, true>), grid2, dim3(256), 0, s, L, T,
                 K, idx, d.wts, (const uint16_t*)w.act, A.act_plane, d.out, d.out32,
                 L.sh_gate ? (const float*)w.shared_out : (const float*)nullptr, l2);
   } else {
-    KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, RPW, UF, false>), grid2, dim3(256), 0, s, L, T,
+    KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, S2_ROWS, RPW, UF, false>), grid2, dim3(256), 0, s, L, T,
                 K, idx, (const float*)nullptr, (const uint16_t*)w.act, A.act_plane, d.out, 0,
                 (const float*)nullptr, l2);
   }
