@@ -2,26 +2,26 @@
 //
 // Replaces the reference's per-token CPU expert MLP (kandiga/metal/kandiga_cpu_expert.m:
 // 355-401 per expert, :471-552 for the K-way fan-out; kandiga/engine.py:727-735 loops it over
-// tokens) and the router/combine around it (moe_block.metal:419-539).  Every distinct expert
-// selected by any token is read from HBM once per layer and applied to all tokens routed to it.
+// tokens) and the router/combine around it (moe_block.metal:419-539).  Each token's distinct
+// selected experts are streamed from HBM once per layer.
 //
 // Two launches per layer.  On MI355X a kernel boundary (~1.6 us) is the cheapest grid-wide
 // barrier: measured agent-scope counter or flag barriers cost 6-28 us for 256-512 workgroups.
 //
-//   dec_stage1_kernel: grid = (distinct-expert slot, block of 4*RW intermediate rows).  Every
-//     workgroup stages x of all tokens in LDS (pair order, with per-chunk sums), recomputes
-//     the routing (DPP arg-max per token) or reads the given indices, and groups the T*K
-//     assignments by expert with a stable rank; workgroup 0 publishes routing and grouping.
-//     Each wave then streams RW gate rows and the same RW up rows of its expert (one 32-code
-//     chunk per lane per step), accumulates q*x with v_dot2_f32_f16 on raw codes, applies
-//     s*2^24*dot + b*sum(x) per chunk, reduces across the wave with DPP and writes
-//     act = silu(gate) * up as two fp16 planes (hi, lo: hi + lo carries ~22 bits) in pair
-//     order.
-//   dec_stage2_kernel: grid = blocks of 64/LPR output rows (LPR lanes per row).  The four
-//     waves split the distinct experts; each lane accumulates w[t,k] * (down row . act) per
-//     token and the waves' partials are added in a fixed order in LDS, so the combine
-//     (moe_block.metal:515-539) is fused and deterministic.  The per-assignment variant writes
-//     y[t,k,:] instead (the switch_mlp contract, engine.py:670-739).
+//   dec_stage1_kernel: grid = tokens x workgroups per token.  Every workgroup routes its token
+//     (DPP arg-max rounds) or reads its given indices, keeps the token's x in registers (pair
+//     order, with per-chunk sums) and loops over (distinct expert, block of 4*RW intermediate
+//     rows) items.  Each wave streams RW gate rows and the same RW up rows of the expert (one
+//     32-code chunk per lane per row), accumulates q*x with v_dot2_f32_f16 on raw codes,
+//     applies s*2^24*dot + b*sum(x) per chunk, reduces all 2*RW values across the wave in one
+//     pass and writes act = silu(gate) * up as two fp16 planes (hi, lo: hi + lo carries ~22
+//     bits) in pair order.
+//   dec_stage2_kernel: grid = blocks of S2_ROWS output rows.  Lanes are (assignment, 32-wide
+//     chunk of the intermediate dimension) over RPW rows of the down projection; each lane
+//     dots its act chunk (hi and lo planes) with the rows' codes, the per-assignment row totals
+//     go to LDS and are combined in k order with the routing weights (moe_block.metal:515-539),
+//     so the fused combine is deterministic.  The per-assignment variant writes y[t,k,:]
+//     instead (the switch_mlp contract, engine.py:670-739).
 #include "kmoe_device.h"
 #include "kmoe_internal.h"
 
@@ -101,348 +101,43 @@ struct Stage1Args {
   const float* logits;      // [T][E] (routing mode) or null
   const int32_t* idx_in;    // [T][K] (given-indices mode) or null
   int T, K;
-  int32_t* idx_out;         // [T][K] routing (workgroup 0), may be null
+  int32_t* idx_out;         // [T][K] routing (first workgroup of each token), may be null
   float* w_out;             // [T][K]
-  int32_t* scalars;         // [0] = distinct experts, [2] = device error flags
+  int32_t* scalars;         // [2] = device error flags
   uint16_t* act;            // [2][T*K][I], row a = assignment t*K + k
   size_t act_plane;
-  int wgs_per_expert;
+  int wgs_per_expert;       // row blocks (items) per expert: I / (4*RW)
+  int wgs_per_token;        // workgroups working on each token
 };
 
-template <int BITS, bool BF16, int ACT, int NT, int CPL, bool ROUTE>
+// Stage 1.  Workgroup b works on token t = b / wgs_per_token only: wave 0 routes the token (or
+// every wave reads its given indices) and shares the K experts through LDS behind the kernel's one
+// barrier; every wave keeps the x chunks its lanes multiply in registers (pair order, with chunk
+// sums).  Lane k < K of each wave holds assignment k's expert; the distinct experts are the lanes
+// whose expert no lower lane also holds (routing never repeats one; given indices may).  Items are
+// (distinct expert, block of 4*RW rows), strided over the token's workgroups; each writes act for
+// every assignment of that expert.  The next item's weights are loaded while the current one is
+// computed (two register stages, unrolled by two so no stage is copied while its loads are in
+// flight).  Weights come through buffer resources made per expert, so the row offset is a scalar
+// and the lane's chunk offset a constant.  Tokens are not grouped by expert: routing one token per
+// workgroup keeps the prologue as short as a single token's, and an expert that two tokens share
+// is read twice (the second read mostly from the memory-side cache).  CPL = x chunks per lane
+// (H <= 64*32*CPL).
+template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE>
 __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
-  extern __shared__ uint32_t dyn[];
-  __shared__ int32_t s_e[DEC_MAX_ASSIGN];
-  __shared__ float s_w[DEC_MAX_ASSIGN];
-  __shared__ int32_t s_perm[DEC_MAX_ASSIGN];
-  __shared__ int32_t s_ptok[DEC_MAX_ASSIGN];
-  __shared__ int32_t s_slot_e[DEC_MAX_ASSIGN];
-  __shared__ int32_t s_slot_p[DEC_MAX_ASSIGN + 1];
-  __shared__ int32_t s_tmp[4];
-
-  const LayerArgs& L = A.L;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int T = A.T, K = A.K, TK = T * K;
-  const int H = L.H, I = L.I, E = L.E;
-  const int nch = H / CHUNK;
-  uint32_t* xs = dyn;                                                  // [T][nch][16]
-  float* xsum = reinterpret_cast<float*>(dyn + (size_t)T * nch * 16);  // [T][nch]
-  const bool lead = blockIdx.x == 0;
-  KMOE_MARK(0, 0);
-
-  // x of every token, pair order, with per-chunk sums.  Each thread's first two chunks are
-  // loaded before the routing code so their latency overlaps the logits loads.
-  const int ntask = T * nch;
-  uint32_t xpre[2][16];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int task = tid + 256 * j;
-    if (task < ntask) load16(A.x + (size_t)(task / nch) * H + (size_t)(task % nch) * CHUNK, xpre[j]);
-  }
-
-  // routing, or the given indices (out-of-range experts are dropped and flagged)
-  if constexpr (ROUTE) {
-    auto publish = [&](int t, int e, float w) {
-      if (lane < K) {
-        s_e[t * K + lane] = e;
-        s_w[t * K + lane] = w;
-        if (lead && A.idx_out) A.idx_out[t * K + lane] = e;
-        if (lead && A.w_out) A.w_out[t * K + lane] = w;
-      }
-    };
-    if (T > 4) {
-      // tokens wave and wave + 4 as two interleaved chains; past the end the second repeats the
-      // first and its result is dropped
-      const int t1 = wave + 4 < T ? wave + 4 : wave;
-      const float* const rows[2] = {A.logits + (size_t)wave * E, A.logits + (size_t)t1 * E};
-      int se[2];
-      float sw[2];
-      KMOE_TOPK_DISPATCH(E, (wave_topk_rows<EPL_, 2>(rows, E, K, se, sw)));
-      publish(wave, se[0], sw[0]);
-      if (wave + 4 < T) publish(wave + 4, se[1], sw[1]);
-    } else if (wave < T) {
-      int se;
-      float sw;
-      KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(A.logits + (size_t)wave * E, E, K, se, sw)));
-      publish(wave, se, sw);
-    }
-  } else {
-    for (int a = tid; a < TK; a += 256) {
-      const int e = A.idx_in[a];
-      s_e[a] = (e >= 0 && e < E) ? e : -1;
-    }
-  }
-  KMOE_MARK(0, 1);
-  for (int task = tid; task < ntask; task += 256) {
-    uint32_t nat[16], pr[16];
-    if (task == tid) {
-#pragma unroll
-      for (int q = 0; q < 16; ++q) nat[q] = xpre[0][q];
-    } else if (task == tid + 256) {
-#pragma unroll
-      for (int q = 0; q < 16; ++q) nat[q] = xpre[1][q];
-    } else {
-      load16(A.x + (size_t)(task / nch) * H + (size_t)(task % nch) * CHUNK, nat);
-    }
-    to_pair_order<BITS>(nat, pr);
-    uint4* dst = reinterpret_cast<uint4*>(xs + (size_t)task * 16);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = make_uint4(pr[4 * q], pr[4 * q + 1], pr[4 * q + 2], pr[4 * q + 3]);
-    float sm = 0.f;
-#pragma unroll
-    for (int m = 0; m < 16; ++m) sm = fdot2(nat[m], ONE2, sm);
-    xsum[task] = sm;
-  }
-  __syncthreads();
-  KMOE_MARK(0, 2);
-  // Stable grouping of the valid assignments by expert: s_perm lists them by (expert, id) and
-  // s_ptok gives each sorted position's token.  Each expert's run is cut into slots of at most
-  // NT assignments (given indices may repeat an expert within a token, so a run can exceed T):
-  // slot s covers positions s_slot_p[s] .. s_slot_p[s+1]-1, all of expert s_slot_e[s].
-  int nvalid, nu, nsl;
-  if (TK <= 64) {
-    if (wave == 0) {  // one wave, lane a holds assignment a: ranks by a radix pass of ballots
-      const int e = lane < TK ? s_e[lane] : -1;
-      const bool valid = e >= 0;
-      const uint64_t below = (1ull << lane) - 1ull;
-      const int nbits = 32 - __clz(max(E - 1, 1));
-      // eq: valid lanes whose expert agrees with mine on the bits seen so far;
-      // less: valid lanes whose expert is smaller
-      uint64_t eq = __ballot(valid);
-      int less = 0;
-      for (int bit = nbits - 1; bit >= 0; --bit) {
-        const bool one = (e >> bit) & 1;
-        const uint64_t ones = __ballot(valid && one);
-        less += one ? __popcll(eq & ~ones) : 0;
-        eq &= one ? ones : ~ones;
-      }
-      const int within = __popcll(eq & below);  // rank inside the expert's run
-      const int r = less + within;
-      const bool first = valid && within == 0;
-      const bool sfirst = valid && within % NT == 0;
-      // slot-opening lanes of smaller experts, by the same radix pass
-      uint64_t eqs = __ballot(sfirst);
-      int sless = 0;
-      for (int bit = nbits - 1; bit >= 0; --bit) {
-        const bool one = (e >> bit) & 1;
-        const uint64_t ones = __ballot(sfirst && one);
-        sless += one ? __popcll(eqs & ~ones) : 0;
-        eqs &= one ? ones : ~ones;
-      }
-      if (valid) {
-        s_perm[r] = lane;
-        s_ptok[r] = lane / K;
-      }
-      if (sfirst) {
-        const int sl = sless + within / NT;
-        s_slot_e[sl] = e;
-        s_slot_p[sl] = r;
-      }
-      const int nv = __popcll(__ballot(valid)), nf = __popcll(__ballot(first));
-      const int ns = __popcll(__ballot(sfirst));
-      if (lane == 0) {
-        s_slot_p[ns] = nv;
-        s_tmp[0] = nv;
-        s_tmp[1] = nf;
-        s_tmp[2] = ns;
-      }
-    }
-    __syncthreads();
-    nvalid = s_tmp[0];
-    nu = s_tmp[1];
-    nsl = s_tmp[2];
-  } else {
-    const int my_e = tid < TK ? s_e[tid] : -1;
-    if (my_e >= 0) {
-      const int key = my_e * DEC_MAX_ASSIGN + tid;
-      int r = 0;
-      for (int b = 0; b < TK; ++b) {
-        const int eb = s_e[b];
-        r += (eb >= 0) & ((eb * DEC_MAX_ASSIGN + b) < key);
-      }
-      s_perm[r] = tid;
-      s_ptok[r] = tid / K;
-    }
-    block_prefix_count(my_e >= 0, s_tmp, &nvalid);  // its barriers also order the s_perm writes
-    int pe = -1, within = 0;
-    if (tid < nvalid) {
-      pe = s_e[s_perm[tid]];
-      int rs = 0;  // start of this expert's run: valid assignments of smaller experts
-      for (int b = 0; b < TK; ++b) {
-        const int eb = s_e[b];
-        rs += (eb >= 0) & (eb < pe);
-      }
-      within = tid - rs;
-    }
-    block_prefix_count(tid < nvalid && within == 0, s_tmp, &nu);
-    const bool sfirst = tid < nvalid && within % NT == 0;
-    const int sl = block_prefix_count(sfirst, s_tmp, &nsl);
-    if (sfirst) {
-      s_slot_e[sl] = pe;
-      s_slot_p[sl] = tid;
-    }
-    if (tid == 0) s_slot_p[nsl] = nvalid;
-    __syncthreads();
-  }
-  if (lead && tid == 0) {
-    A.scalars[0] = nu;
-    if (nvalid != TK) atomicOr(&A.scalars[2], DEVERR_BAD_EXPERT);
-  }
-
-  KMOE_MARK(0, 3);
-  // (slot, block of 4*RW rows) items, grid-strided over the workgroups.  The weights of the
-  // next item are loaded while the current one is computed (two register stages, unrolled by
-  // two so no stage is copied while its loads are in flight).  Weights come through buffer
-  // resources made per expert: the row offset is a scalar and the lane's chunk offset a
-  // constant, so no per-load address arithmetic runs on the vector ALU.
-  constexpr int RW = stage1_rw(NT);
-  constexpr int V = 2 * RW;  // reduced values per token: gate then up, of RW rows
-  const int wpe = A.wgs_per_expert;
-  const int nitems = nsl * wpe;
-  const uint32_t rbytes = (uint32_t)H * BITS / 8;
-  const int ng = H / GROUP;
-  const uint32_t wbytes = (uint32_t)I * rbytes, sbytes = (uint32_t)I * ng * 2;
-  const int wv = __builtin_amdgcn_readfirstlane(wave);
-  uint32_t cvo[CPL], svo[CPL];
-#pragma unroll
-  for (int q = 0; q < CPL; ++q) {
-    const int c = min(lane + 64 * q, nch - 1);  // lanes past the row's end reload its last chunk
-    cvo[q] = (uint32_t)c * Bits<BITS>::chunk_bytes;
-    svo[q] = (uint32_t)(c >> 1) * 2u;
-  }
-  struct WStage {
-    uint32_t gd[CPL][RW][4], ud[CPL][RW][4];
-    uint16_t gsc[CPL][RW], gbi[CPL][RW], usc[CPL][RW], ubi[CPL][RW];
-  };
-  auto load_item = [&](int item, WStage& W) {
-    const int sl = item / wpe;
-    const int rb = item - sl * wpe;
-    const int e = __builtin_amdgcn_readfirstlane(s_slot_e[sl]);
-    const int ib = rb * (4 * RW) + wv * RW;
-    const auto gw = make_rsrc(L.gate.w + (size_t)e * L.gate.w_stride, wbytes);
-    const auto uw = make_rsrc(L.up.w + (size_t)e * L.up.w_stride, wbytes);
-    const auto gs = make_rsrc(L.gate.s + (size_t)e * L.gate.s_stride, sbytes);
-    const auto gb = make_rsrc(L.gate.b + (size_t)e * L.gate.s_stride, sbytes);
-    const auto us = make_rsrc(L.up.s + (size_t)e * L.up.s_stride, sbytes);
-    const auto ub = make_rsrc(L.up.b + (size_t)e * L.up.s_stride, sbytes);
-#pragma unroll
-    for (int q = 0; q < CPL; ++q) {
-#pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        const uint32_t wo = (uint32_t)(ib + r) * rbytes, so = (uint32_t)(ib + r) * ng * 2u;
-        buf_chunk<BITS>(gw, cvo[q], wo, W.gd[q][r]);
-        buf_chunk<BITS>(uw, cvo[q], wo, W.ud[q][r]);
-        W.gsc[q][r] = buf_u16(gs, svo[q], so);
-        W.gbi[q][r] = buf_u16(gb, svo[q], so);
-        W.usc[q][r] = buf_u16(us, svo[q], so);
-        W.ubi[q][r] = buf_u16(ub, svo[q], so);
-      }
-    }
-  };
-  auto compute_item = [&](int item, const WStage& W) {
-    const int sl = item / wpe;
-    const int rb = item - sl * wpe;
-    const int p0 = __builtin_amdgcn_readfirstlane(s_slot_p[sl]);
-    const int na = __builtin_amdgcn_readfirstlane(s_slot_p[sl + 1]) - p0;  // 1..NT
-    const int ib = rb * (4 * RW) + wv * RW;
-    // act column of the row this lane stores after the reduction (row r sits in lane group r)
-    int col = 0;
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      const int i = ib + r;
-      const int cr = (i & ~31) + pairpos<BITS>(i & 31);
-      col = (lane >> (V == 8 ? 3 : 4)) == r ? cr : col;
-    }
-    // acc[j][gu * RW + r]: token j's gate (gu = 0) or up (gu = 1) partial of row r
-    float acc[NT][V];
-#pragma unroll
-    for (int q = 0; q < CPL; ++q) {
-      const int c = lane + 64 * q;
-      const int cc = min(c, nch - 1);
-      const bool cv = c < nch;
-#pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        uint32_t cg[16], cu[16];
-        unpack_chunk<BITS, false>(W.gd[q][r], cg);
-        unpack_chunk<BITS, false>(W.ud[q][r], cu);
-        const float sg = scale_to_f32<BF16>(W.gsc[q][r]) * TWO24, bg = scale_to_f32<BF16>(W.gbi[q][r]);
-        const float su = scale_to_f32<BF16>(W.usc[q][r]) * TWO24, bu = scale_to_f32<BF16>(W.ubi[q][r]);
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          if (j < na) {
-            const int t = __builtin_amdgcn_readfirstlane(s_ptok[p0 + j]);
-            uint32_t xv[16];
-            load16(xs + ((size_t)t * nch + cc) * 16, xv);
-            const float xsm = xsum[t * nch + cc];
-            float dg = sg * chunk_dot(cg, xv) + bg * xsm;
-            float du = su * chunk_dot(cu, xv) + bu * xsm;
-            if (!cv) dg = du = 0.f;
-            if (q == 0) {
-              acc[j][r] = dg;
-              acc[j][RW + r] = du;
-            } else {
-              acc[j][r] += dg;
-              acc[j][RW + r] += du;
-            }
-          }
-        }
-      }
-    }
-    // lane groups 0..RW-1 hold the gate totals of rows 0..RW-1, groups RW..2RW-1 the up totals:
-    // one swap of the wave halves puts each row's up total beside its gate total
-    const bool store_lane = lane < 32 && (lane & (64 / V - 1)) == 0;
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      if (j < na) {
-        const float g = wave_sum_multi<V>(acc[j]);
-        const float u = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(g), __float_as_uint(g),
-                                                                         false, false)[1]);
-        const int asg = __builtin_amdgcn_readfirstlane(s_perm[p0 + j]);
-        if (store_lane) {
-          const float a = activate<ACT>(g, u);
-          const _Float16 hi = (_Float16)a;
-          const _Float16 lo = (_Float16)(a - (float)hi);
-          const size_t o = (size_t)asg * I + col;
-          A.act[o] = __builtin_bit_cast(uint16_t, hi);
-          A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
-        }
-      }
-    }
-    KMOE_MARK(0, 4);
-  };
-  WStage W0, W1;
-  const int step = gridDim.x;
-  int item = blockIdx.x;
-  if (item < nitems) load_item(item, W0);
-  for (; item < nitems; item += 2 * step) {
-    if (item + step < nitems) load_item(item + step, W1);
-    compute_item(item, W0);
-    if (item + step >= nitems) break;
-    if (item + 2 * step < nitems) load_item(item + 2 * step, W0);
-    compute_item(item + step, W1);
-  }
-  KMOE_MARK(0, 5);
-}
-
-// Stage 1 for a single token.  Wave 0 routes the token (or every wave reads the given indices)
-// and shares the K experts through LDS behind the kernel's one barrier; every wave keeps the x
-// chunks its lanes multiply in registers (pair order, with chunk sums), so x is not staged in
-// LDS.  Lane k < K of each wave holds assignment k's expert.  The distinct experts are the lanes whose expert no lower lane also holds (routing
-// never repeats one; given indices may), and each (distinct expert, block of 4*RW rows) item
-// writes act for every assignment of that expert.  CPL = x chunks per lane (H <= 64*32*CPL).
-template <int BITS, bool BF16, int ACT, int CPL, bool ROUTE>
-__global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) {
   const LayerArgs& L = A.L;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int K = A.K, H = L.H, I = L.I, E = L.E;
   const int nch = H / CHUNK;
+  const int t = blockIdx.x / A.wgs_per_token;
+  const int lb = blockIdx.x - t * A.wgs_per_token;
   KMOE_MARK(0, 0);
   uint32_t xr[CPL][16];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = lane + 64 * j;
     if (c < nch) {
-      load16(A.x + (size_t)c * CHUNK, xr[j]);
+      load16(A.x + (size_t)t * H + (size_t)c * CHUNK, xr[j]);
     } else {
 #pragma unroll
       for (int m = 0; m < 16; ++m) xr[j][m] = 0u;
@@ -455,12 +150,12 @@ __global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) 
     __shared__ int32_t s_sel[16];
     if (wave == 0) {
       float myw;
-      KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(A.logits, E, K, my, myw)));
+      KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(A.logits + (size_t)t * E, E, K, my, myw)));
       if (lane < K) {
         s_sel[lane] = my;
-        if (blockIdx.x == 0) {
-          if (A.idx_out) A.idx_out[lane] = my;
-          if (A.w_out) A.w_out[lane] = myw;
+        if (lb == 0) {
+          if (A.idx_out) A.idx_out[t * K + lane] = my;
+          if (A.w_out) A.w_out[t * K + lane] = myw;
         }
       }
     }
@@ -468,7 +163,7 @@ __global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) 
     my = lane < K ? s_sel[lane] : -1;
   } else {
     if (lane < K) {
-      const int e = A.idx_in[lane];
+      const int e = A.idx_in[t * K + lane];
       my = (e >= 0 && e < E) ? e : -1;
     }
   }
@@ -494,79 +189,94 @@ __global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) 
   }
   const uint64_t first_m = __ballot(first);
   const int nu = __popcll(first_m);
-  if (blockIdx.x == 0 && tid == 0) {
-    A.scalars[0] = nu;
-    if (__popcll(valid_m) != K) atomicOr(&A.scalars[2], DEVERR_BAD_EXPERT);
-  }
+  if (lb == 0 && tid == 0 && __popcll(valid_m) != K) atomicOr(&A.scalars[2], DEVERR_BAD_EXPERT);
   KMOE_MARK(0, 3);
 
-  const int nitems = nu * A.wgs_per_expert;
-  constexpr int V = 2 * DEC_RW;  // reduced values: gate then up, of DEC_RW rows
+  constexpr int V = 2 * RW;  // reduced values per item: gate then up, of RW rows
+  const int wpe = A.wgs_per_expert;
+  const int nitems = nu * wpe;
   const uint32_t rbytes = (uint32_t)H * BITS / 8;
   const int ng = H / GROUP;
   const uint32_t wbytes = (uint32_t)I * rbytes, sbytes = (uint32_t)I * ng * 2;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const bool store_lane = lane < 32 && (lane & (64 / V - 1)) == 0;
-  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
-    const int u = item / A.wgs_per_expert;
-    const int rb = item - u * A.wgs_per_expert;
+  uint32_t cvo[CPL], svo[CPL];
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) {
+    const int c = min(lane + 64 * q, nch - 1);  // lanes past the row's end reload its last chunk
+    cvo[q] = (uint32_t)c * Bits<BITS>::chunk_bytes;
+    svo[q] = (uint32_t)(c >> 1) * 2u;
+  }
+  // expert of the token's u-th distinct expert (uniform)
+  auto item_expert = [&](int u) {
     uint64_t fm = first_m;
     for (int q = 0; q < u; ++q) fm &= fm - 1ull;
-    const int e = __builtin_amdgcn_readlane(my, (int)__builtin_ctzll(fm));
-    const uint64_t amask = __ballot(my == e);
-    const int ib = rb * (4 * DEC_RW) + wv * DEC_RW;
-    // buffer resources of this expert: scalar row offsets, constant per-lane chunk offsets
+    return __builtin_amdgcn_readlane(my, (int)__builtin_ctzll(fm));
+  };
+  struct WStage {
+    uint32_t gd[CPL][RW][4], ud[CPL][RW][4];
+    uint16_t gsc[CPL][RW], gbi[CPL][RW], usc[CPL][RW], ubi[CPL][RW];
+  };
+  auto load_item = [&](int item, WStage& W) {
+    const int u = item / wpe;
+    const int rb = item - u * wpe;
+    const int e = item_expert(u);
+    const int ib = rb * (4 * RW) + wv * RW;
     const auto gw = make_rsrc(L.gate.w + (size_t)e * L.gate.w_stride, wbytes);
     const auto uw = make_rsrc(L.up.w + (size_t)e * L.up.w_stride, wbytes);
     const auto gs = make_rsrc(L.gate.s + (size_t)e * L.gate.s_stride, sbytes);
     const auto gb = make_rsrc(L.gate.b + (size_t)e * L.gate.s_stride, sbytes);
     const auto us = make_rsrc(L.up.s + (size_t)e * L.up.s_stride, sbytes);
     const auto ub = make_rsrc(L.up.b + (size_t)e * L.up.s_stride, sbytes);
-    uint32_t gd[CPL][DEC_RW][4], ud[CPL][DEC_RW][4];
-    uint16_t gsc[CPL][DEC_RW], gbi[CPL][DEC_RW], usc[CPL][DEC_RW], ubi[CPL][DEC_RW];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = min(lane + 64 * j, nch - 1);  // lanes past the row's end reload its last chunk
-      const uint32_t cvo = (uint32_t)c * Bits<BITS>::chunk_bytes, svo = (uint32_t)(c >> 1) * 2u;
+    for (int q = 0; q < CPL; ++q) {
 #pragma unroll
-      for (int r = 0; r < DEC_RW; ++r) {
+      for (int r = 0; r < RW; ++r) {
         const uint32_t wo = (uint32_t)(ib + r) * rbytes, so = (uint32_t)(ib + r) * ng * 2u;
-        buf_chunk<BITS>(gw, cvo, wo, gd[j][r]);
-        buf_chunk<BITS>(uw, cvo, wo, ud[j][r]);
-        gsc[j][r] = buf_u16(gs, svo, so);
-        gbi[j][r] = buf_u16(gb, svo, so);
-        usc[j][r] = buf_u16(us, svo, so);
-        ubi[j][r] = buf_u16(ub, svo, so);
+        buf_chunk<BITS>(gw, cvo[q], wo, W.gd[q][r]);
+        buf_chunk<BITS>(uw, cvo[q], wo, W.ud[q][r]);
+        W.gsc[q][r] = buf_u16(gs, svo[q], so);
+        W.gbi[q][r] = buf_u16(gb, svo[q], so);
+        W.usc[q][r] = buf_u16(us, svo[q], so);
+        W.ubi[q][r] = buf_u16(ub, svo[q], so);
       }
     }
+  };
+  const bool store_lane = lane < 32 && (lane & (64 / V - 1)) == 0;
+  auto compute_item = [&](int item, const WStage& W) {
+    const int u = item / wpe;
+    const int rb = item - u * wpe;
+    const int e = item_expert(u);
+    const uint64_t amask = __ballot(my == e);
+    const int ib = rb * (4 * RW) + wv * RW;
     // act column of the row this lane stores after the reduction (row r sits in lane group r)
     int col = 0;
 #pragma unroll
-    for (int r = 0; r < DEC_RW; ++r) {
+    for (int r = 0; r < RW; ++r) {
       const int i = ib + r;
       const int cr = (i & ~31) + pairpos<BITS>(i & 31);
       col = (lane >> (V == 8 ? 3 : 4)) == r ? cr : col;
     }
-    // acc[gu * DEC_RW + r]: gate (gu = 0) or up (gu = 1) partial of row r
+    // acc[gu * RW + r]: gate (gu = 0) or up (gu = 1) partial of row r
     float acc[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[v] = 0.f;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      if (lane + 64 * j < nch) {
+    for (int q = 0; q < CPL; ++q) {
+      if (lane + 64 * q < nch) {
 #pragma unroll
-        for (int r = 0; r < DEC_RW; ++r) {
+        for (int r = 0; r < RW; ++r) {
           uint32_t cg[16], cu[16];
-          unpack_chunk<BITS, false>(gd[j][r], cg);
-          unpack_chunk<BITS, false>(ud[j][r], cu);
-          acc[r] += scale_to_f32<BF16>(gsc[j][r]) * TWO24 * chunk_dot(cg, xp[j]) + scale_to_f32<BF16>(gbi[j][r]) * xs[j];
-          acc[DEC_RW + r] +=
-              scale_to_f32<BF16>(usc[j][r]) * TWO24 * chunk_dot(cu, xp[j]) + scale_to_f32<BF16>(ubi[j][r]) * xs[j];
+          unpack_chunk<BITS, false>(W.gd[q][r], cg);
+          unpack_chunk<BITS, false>(W.ud[q][r], cu);
+          acc[r] += scale_to_f32<BF16>(W.gsc[q][r]) * TWO24 * chunk_dot(cg, xp[q]) +
+                    scale_to_f32<BF16>(W.gbi[q][r]) * xs[q];
+          acc[RW + r] += scale_to_f32<BF16>(W.usc[q][r]) * TWO24 * chunk_dot(cu, xp[q]) +
+                         scale_to_f32<BF16>(W.ubi[q][r]) * xs[q];
         }
       }
     }
-    // lane groups 0..DEC_RW-1 hold the gate totals, DEC_RW..2*DEC_RW-1 the up totals: one swap
-    // of the wave halves puts each row's up total beside its gate total
+    // lane groups 0..RW-1 hold the gate totals and RW..2RW-1 the up totals: one swap of the
+    // wave halves puts each row's up total beside its gate total
     const float g = wave_sum_multi<V>(acc);
     const float uu =
         __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(g), __float_as_uint(g), false, false)[1]);
@@ -575,16 +285,26 @@ __global__ __launch_bounds__(256) void dec_stage1_t1_kernel(const Stage1Args A) 
       const _Float16 hi = (_Float16)a;
       const _Float16 lo = (_Float16)(a - (float)hi);
       for (uint64_t m = amask; m; m &= m - 1ull) {  // every assignment of this expert (repeats are rare)
-        const size_t o = (size_t)__builtin_ctzll(m) * I + col;
+        const size_t o = (size_t)(t * K + __builtin_ctzll(m)) * I + col;
         A.act[o] = __builtin_bit_cast(uint16_t, hi);
         A.act[A.act_plane + o] = __builtin_bit_cast(uint16_t, lo);
       }
     }
     KMOE_MARK(0, 4);
+  };
+  WStage W0, W1;
+  const int step = A.wgs_per_token;
+  int item = lb;
+  if (item < nitems) load_item(item, W0);
+  for (; item < nitems; item += 2 * step) {
+    if (item + step < nitems) load_item(item + step, W1);
+    compute_item(item, W0);
+    if (item + step >= nitems) break;
+    if (item + 2 * step < nitems) load_item(item + 2 * step, W0);
+    compute_item(item + step, W1);
   }
   KMOE_MARK(0, 5);
 }
-
 
 // Stage 2.  Lane (g, c) of a wave works on assignment g of its unit and 32-wide chunk c of the
 // intermediate dimension, for RPW consecutive output rows: each act chunk is loaded once per
@@ -780,19 +500,9 @@ static int lpa_log2_for(int I) {
   return l;
 }
 
-size_t decode_lds_bytes(const LayerConfig& c, int T) {
-  const size_t nch = (size_t)c.args.H / CHUNK;
-  return (size_t)T * nch * 16 * 4 + (size_t)T * nch * 4;
-}
-
 template <typename KERN>
-static hipError_t launch_stage1(KERN k1, int grid, size_t lds, hipStream_t s, const Stage1Args& A) {
-  if (lds > 65536) {
-    hipError_t ae =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(k1), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (ae != hipSuccess) return ae;
-  }
-  KMOE_LAUNCH("dec_stage1_kernel", k1, dim3(grid), dim3(256), (uint32_t)lds, s, A);
+static hipError_t launch_stage1(KERN k1, int grid, hipStream_t s, const Stage1Args& A) {
+  KMOE_LAUNCH("dec_stage1_kernel", k1, dim3(grid), dim3(256), 0, s, A);
   return hipGetLastError();
 }
 
@@ -801,6 +511,9 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   const LayerArgs& L = c.args;
   const int K = c.top_k, T = d.T;
   const Work& w = *d.w;
+  const int nch = L.H / CHUNK;
+  if (nch > 128) return hipErrorInvalidValue;  // x chunks of a token live in two registers per lane at most
+  constexpr int RW = NT == 1 ? DEC_RW : stage1_rw(NT);
   Stage1Args A;
   A.L = L;
   A.x = d.x;
@@ -813,28 +526,18 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   A.scalars = w.scalars;
   A.act = w.act;
   A.act_plane = (size_t)T * K * L.I;
-  A.wgs_per_expert = L.I / (4 * (NT == 1 ? DEC_RW : stage1_rw(NT)));
-  // at most two workgroups per CU: every workgroup repeats the routing and x staging, so
-  // the grid stays resident and loops over the (expert, row block) items instead
-  const int grid1 = min(min(T * K, L.E) * A.wgs_per_expert, 2 * cu_count());
-  const size_t lds1 = decode_lds_bytes(c, T);
-  const int nch = L.H / CHUNK;
+  A.wgs_per_expert = L.I / (4 * RW);
+  // at most two workgroups per CU in all: every workgroup repeats its token's routing, so the
+  // grid stays resident and loops over the token's (expert, row block) items instead
+  A.wgs_per_token = max(1, min(min(K, L.E) * A.wgs_per_expert, 2 * cu_count() / T));
+  const int grid1 = T * A.wgs_per_token;
   hipError_t err;
-  if (NT == 1 && nch <= 128) {
-    if (nch <= 64)
-      err = d.logits ? launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 1, true>, grid1, 0, s, A)
-                     : launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 1, false>, grid1, 0, s, A);
-    else
-      err = d.logits ? launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 2, true>, grid1, 0, s, A)
-                     : launch_stage1(&dec_stage1_t1_kernel<BITS, BF16, ACT, 2, false>, grid1, 0, s, A);
-  } else {
-    if (nch <= 64)
-      err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, 1, true>, grid1, lds1, s, A)
-                     : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, 1, false>, grid1, lds1, s, A);
-    else
-      err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, 2, true>, grid1, lds1, s, A)
-                     : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, NT, 2, false>, grid1, lds1, s, A);
-  }
+  if (nch <= 64)
+    err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true>, grid1, s, A)
+                   : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false>, grid1, s, A);
+  else
+    err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true>, grid1, s, A)
+                   : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false>, grid1, s, A);
   if (err != hipSuccess) return err;
   const int l2 = lpa_log2_for(L.I);
   // output rows per workgroup and per unit: the single-token layer has few units, so a unit's

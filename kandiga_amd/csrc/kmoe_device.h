@@ -341,103 +341,71 @@ __device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// Top-K of NR tokens' router logits by one wave (moe_block.metal:479-503 semantics): order by
+// Top-K of one token's router logits by one wave (moe_block.metal:479-503 semantics): order by
 // logit descending, equal logits to the lower index; weights exp(l_k - l_max) / sum_j
-// exp(l_j - l_max), summed in k order.  Each lane holds EPL logits per token (EPL * 64 >= E),
-// sorted once by (key desc, index asc).  A round is a 32-bit DPP max over the lanes' head keys; a
-// ballot finds the lanes holding it, and only when two lanes hold the same logit does a second
-// max over the inverted indices pick the lower index.  The winning lane then pops its head.
-// Index e lives in lane e % 64, so the winner's lane follows from its index.  The NR tokens'
-// rounds are independent chains, so their DPP latencies overlap.
-// Lane k < K returns token r's k-th expert in sel[r] and its weight in selw[r]; other lanes
-// get -1, 0.
-template <int EPL, int NR>
-__device__ __forceinline__ void wave_topk_rows(const float* const (&row)[NR], int E, int K, int (&sel)[NR],
-                                               float (&selw)[NR]) {
+// exp(l_j - l_max), summed in k order.  Each lane holds EPL logits (EPL * 64 >= E), sorted once
+// by (key desc, index asc).  A round is a 32-bit DPP max over the lanes' head keys; a ballot
+// finds the lanes holding it, and only when two lanes hold the same logit does a second max
+// over the inverted indices pick the lower index.  The winning lane then pops its head.
+// Index e lives in lane e % 64, so the winner's lane follows from its index.
+// Lane k < K returns the k-th expert in `sel` and its weight in `selw`; other lanes get -1, 0.
+template <int EPL>
+__device__ __forceinline__ void wave_topk_regs(const float* __restrict__ row, int E, int K, int& sel, float& selw) {
   const int lane = threadIdx.x & 63;
-  uint32_t kh[NR][EPL], ke[NR][EPL];  // key, ~index (larger ~index = lower index); padding: key 0, ~index 0
+  uint32_t kh[EPL], ke[EPL];  // key, ~index (larger ~index = lower index); padding: key 0, ~index 0
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-#pragma unroll
-    for (int m = 0; m < EPL; ++m) {
-      const int e = lane + 64 * m;
-      const float v = e < E ? row[r][e] : 0.0f;
-      kh[r][m] = e < E ? logit_key(v) : 0u;
-      ke[r][m] = e < E ? ~(uint32_t)e : 0u;
-    }
+  for (int m = 0; m < EPL; ++m) {
+    const int e = lane + 64 * m;
+    const float v = e < E ? row[e] : 0.0f;
+    kh[m] = e < E ? logit_key(v) : 0u;
+    ke[m] = e < E ? ~(uint32_t)e : 0u;
   }
   // odd-even transposition sort, descending by (key, ~index)
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
+  for (int pass = 0; pass < EPL; ++pass) {
 #pragma unroll
-    for (int pass = 0; pass < EPL; ++pass) {
-#pragma unroll
-      for (int j = pass & 1; j + 1 < EPL; j += 2) {
-        const bool sw = kh[r][j + 1] > kh[r][j] || (kh[r][j + 1] == kh[r][j] && ke[r][j + 1] > ke[r][j]);
-        const uint32_t h0 = kh[r][j], e0 = ke[r][j];
-        kh[r][j] = sw ? kh[r][j + 1] : h0;
-        ke[r][j] = sw ? ke[r][j + 1] : e0;
-        kh[r][j + 1] = sw ? h0 : kh[r][j + 1];
-        ke[r][j + 1] = sw ? e0 : ke[r][j + 1];
-      }
+    for (int j = pass & 1; j + 1 < EPL; j += 2) {
+      const bool sw = kh[j + 1] > kh[j] || (kh[j + 1] == kh[j] && ke[j + 1] > ke[j]);
+      const uint32_t h0 = kh[j], e0 = ke[j];
+      kh[j] = sw ? kh[j + 1] : h0;
+      ke[j] = sw ? ke[j + 1] : e0;
+      kh[j + 1] = sw ? h0 : kh[j + 1];
+      ke[j + 1] = sw ? e0 : ke[j + 1];
     }
   }
-  int my[NR];
-  float my_l[NR];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    my[r] = 0;
-    my_l[r] = 0.0f;
-  }
+  int my = 0;
+  float my_l = 0.0f;
   for (int k = 0; k < K; ++k) {
-    uint32_t m[NR];
+    const uint32_t m = wave_max_u32_dpp(kh[0]);
+    const uint64_t holders = __ballot(kh[0] == m);
+    uint32_t einv;
+    if (__popcll(holders) == 1) {
+      einv = (uint32_t)__builtin_amdgcn_readlane((int)ke[0], (int)__builtin_ctzll(holders));
+    } else {
+      einv = wave_max_u32_dpp(kh[0] == m ? ke[0] : 0u);
+    }
+    const int e = (int)~einv;
+    if (lane == (e & 63)) {  // pop the head
 #pragma unroll
-    for (int r = 0; r < NR; ++r) m[r] = wave_max_u32_dpp(kh[r][0]);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const uint64_t holders = __ballot(kh[r][0] == m[r]);
-      uint32_t einv;
-      if (__popcll(holders) == 1) {
-        einv = (uint32_t)__builtin_amdgcn_readlane((int)ke[r][0], (int)__builtin_ctzll(holders));
-      } else {
-        einv = wave_max_u32_dpp(kh[r][0] == m[r] ? ke[r][0] : 0u);
+      for (int j = 0; j + 1 < EPL; ++j) {
+        kh[j] = kh[j + 1];
+        ke[j] = ke[j + 1];
       }
-      const int e = (int)~einv;
-      if (lane == (e & 63)) {  // pop the head
-#pragma unroll
-        for (int j = 0; j + 1 < EPL; ++j) {
-          kh[r][j] = kh[r][j + 1];
-          ke[r][j] = ke[r][j + 1];
-        }
-        kh[r][EPL - 1] = 0u;
-        ke[r][EPL - 1] = 0u;
-      }
-      if (lane == k) {
-        my[r] = e;
-        my_l[r] = logit_from_key(m[r]);
-      }
+      kh[EPL - 1] = 0u;
+      ke[EPL - 1] = 0u;
+    }
+    if (lane == k) {
+      my = e;
+      my_l = logit_from_key(m);
     }
   }
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const float l0 = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(my_l[r])));
-    const float ex = lane < K ? expf(my_l[r] - l0) : 0.0f;
-    float sum = 0.0f;
-    for (int k = 0; k < K; ++k)
-      sum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(ex), k));
-    sel[r] = lane < K ? my[r] : -1;
-    selw[r] = lane < K ? ex / sum : 0.0f;
-  }
-}
-
-template <int EPL>
-__device__ __forceinline__ void wave_topk_regs(const float* __restrict__ row, int E, int K, int& sel, float& selw) {
-  const float* const rows[1] = {row};
-  int s[1];
-  float w[1];
-  wave_topk_rows<EPL, 1>(rows, E, K, s, w);
-  sel = s[0];
-  selw = w[0];
+  const float l0 = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(my_l)));
+  const float ex = lane < K ? expf(my_l - l0) : 0.0f;
+  float sum = 0.0f;
+  for (int k = 0; k < K; ++k)
+    sum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(ex), k));
+  sel = lane < K ? my : -1;
+  selw = lane < K ? ex / sum : 0.0f;
 }
 
 // wave_topk_regs with the results stored: lanes k < K write idx_out[k] / w_out[k] (either may

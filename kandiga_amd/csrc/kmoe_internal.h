@@ -59,7 +59,6 @@ struct Work {
 constexpr int PERM_TILE = 1024;   // assignments per permutation tile
 constexpr int GEMM_BM = 128;      // assignment rows per grouped-GEMM tile
 constexpr int DEC_MAX_TOKENS = 8; // largest batch served by the GEMV path
-constexpr int DEC_MAX_ASSIGN = 256;   // grouping arrays of the decode stage 1
 constexpr int DEC_STAGE2_ASSIGN = 128; // assignments held in two lane slots by decode stage 2
 
 // Device error flag bits (Work::scalars[2]).
@@ -114,6 +113,5 @@ hipError_t launch_shared(const LayerConfig& c, const uint16_t* x, int T, const W
 hipError_t launch_dequantize(const LayerConfig& c, int proj, int expert, int row0, int nrows, uint8_t* codes,
                              uint16_t* wf16, hipStream_t s);
 
-size_t decode_lds_bytes(const LayerConfig& c, int T);
 
 }  // namespace kmoe
