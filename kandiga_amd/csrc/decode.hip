@@ -29,7 +29,7 @@ namespace kmoe {
 
 // Phase trace, compiled in only with -DKMOE_PHASE_TRACE: thread 0 of each workgroup stores the
 // 100 MHz s_memrealtime clock at the marked points of the two decode kernels, read back with
-// kmoe_phase_trace_dump().  Marks, stage 1: 0 entry, 1 routed, 2 x staged, 3 grouped,
+// kmoe_phase_trace_dump().  Marks, stage 1: 0 entry, 1 routed (wave 0), 2 x permuted, 3 experts known,
 // 4 item computed, 5 end; stage 2: 0 entry, 1 metadata, 2 experts done, 3 end.
 #ifdef KMOE_PHASE_TRACE
 constexpr int TRACE_WGS = 4096;
@@ -144,27 +144,18 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
     }
   }
   int my = -1;
-  if constexpr (ROUTE) {
-    // one routing wave per workgroup: redundant copies in the other waves would share SIMDs
-    // with it and stretch its latency; they wait at the barrier instead
-    __shared__ int32_t s_sel[16];
-    if (wave == 0) {
-      float myw;
-      KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(A.logits + (size_t)t * E, E, K, my, myw)));
-      if (lane < K) {
-        s_sel[lane] = my;
-        if (lb == 0) {
-          if (A.idx_out) A.idx_out[t * K + lane] = my;
-          if (A.w_out) A.w_out[t * K + lane] = myw;
-        }
-      }
-    }
-    __syncthreads();
-    my = lane < K ? s_sel[lane] : -1;
-  } else {
+  // one routing wave per workgroup: redundant copies in the other waves would share SIMDs with
+  // it and stretch its latency; they permute their x chunks and wait at the barrier instead
+  __shared__ int32_t s_sel[16];
+  if (ROUTE && wave == 0) {
+    float myw;
+    KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(A.logits + (size_t)t * E, E, K, my, myw)));
     if (lane < K) {
-      const int e = A.idx_in[t * K + lane];
-      my = (e >= 0 && e < E) ? e : -1;
+      s_sel[lane] = my;
+      if (lb == 0) {
+        if (A.idx_out) A.idx_out[t * K + lane] = my;
+        if (A.w_out) A.w_out[t * K + lane] = myw;
+      }
     }
   }
   KMOE_MARK(0, 1);
@@ -177,6 +168,20 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
 #pragma unroll
     for (int m = 0; m < 16; ++m) sm = fdot2(xr[j][m], ONE2, sm);
     xs[j] = sm;
+    // keep this work ahead of the barrier: sunk into the item loop it would wait behind the
+    // first item's weight loads
+#pragma unroll
+    for (int m = 0; m < 16; ++m) asm volatile("" : "+v"(xp[j][m]));
+    asm volatile("" : "+v"(xs[j]));
+  }
+  if constexpr (ROUTE) {
+    __syncthreads();
+    my = lane < K ? s_sel[lane] : -1;
+  } else {
+    if (lane < K) {
+      const int e = A.idx_in[t * K + lane];
+      my = (e >= 0 && e < E) ? e : -1;
+    }
   }
   KMOE_MARK(0, 2);
   const uint64_t valid_m = __ballot(my >= 0);

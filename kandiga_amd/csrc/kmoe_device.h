@@ -349,15 +349,27 @@ __device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
 // over the inverted indices pick the lower index.  The winning lane then pops its head.
 // Index e lives in lane e % 64, so the winner's lane follows from its index.
 // Lane k < K returns the k-th expert in `sel` and its weight in `selw`; other lanes get -1, 0.
+constexpr int TOPK_MAX_EPL = 16;  // logits per lane for up to 1024 experts
+
+// Loads lane l's logits row[l + 64m] (m < ceil(E/64), zero past E) for wave_topk_vals, so the
+// loads can be issued early and other work done while they are in flight.
+__device__ __forceinline__ void wave_load_logits(const float* __restrict__ row, int E, float (&lv)[TOPK_MAX_EPL]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < TOPK_MAX_EPL; ++m) {
+    const int e = lane + 64 * m;
+    lv[m] = 64 * m < E && e < E ? row[e] : 0.0f;
+  }
+}
+
 template <int EPL>
-__device__ __forceinline__ void wave_topk_regs(const float* __restrict__ row, int E, int K, int& sel, float& selw) {
+__device__ __forceinline__ void wave_topk_vals(const float (&lv)[TOPK_MAX_EPL], int E, int K, int& sel, float& selw) {
   const int lane = threadIdx.x & 63;
   uint32_t kh[EPL], ke[EPL];  // key, ~index (larger ~index = lower index); padding: key 0, ~index 0
 #pragma unroll
   for (int m = 0; m < EPL; ++m) {
     const int e = lane + 64 * m;
-    const float v = e < E ? row[e] : 0.0f;
-    kh[m] = e < E ? logit_key(v) : 0u;
+    kh[m] = e < E ? logit_key(lv[m]) : 0u;
     ke[m] = e < E ? ~(uint32_t)e : 0u;
   }
   // odd-even transposition sort, descending by (key, ~index)
@@ -406,6 +418,13 @@ __device__ __forceinline__ void wave_topk_regs(const float* __restrict__ row, in
     sum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(ex), k));
   sel = lane < K ? my : -1;
   selw = lane < K ? ex / sum : 0.0f;
+}
+
+template <int EPL>
+__device__ __forceinline__ void wave_topk_regs(const float* __restrict__ row, int E, int K, int& sel, float& selw) {
+  float lv[TOPK_MAX_EPL];
+  wave_load_logits(row, E, lv);
+  wave_topk_vals<EPL>(lv, E, K, sel, selw);
 }
 
 // wave_topk_regs with the results stored: lanes k < K write idx_out[k] / w_out[k] (either may
