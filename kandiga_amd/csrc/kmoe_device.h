@@ -90,30 +90,50 @@ __device__ __forceinline__ uint32_t mask_or(uint32_t v) {
   }
 }
 
+// Pair P (0..15) of a 3-bit chunk.  Pairs 0-3 come from d0, 4-8 from d1, 9-12 from d2 (one
+// packed shift each); 13-15 hold the codes that straddle dword boundaries or sit in the other
+// half-word.
+template <int P, bool MAGIC>
+__device__ __forceinline__ uint32_t pair3(uint32_t d0, uint32_t d1, uint32_t d2) {
+  constexpr uint32_t M = 0x00070007u, O = MAGIC ? 0x64006400u : 0u;
+  if constexpr (P < 4) {
+    return mask_or<M, O>(pk_shr(d0, 3 * P, 3 * P + 2));
+  } else if constexpr (P < 9) {
+    return mask_or<M, O>(pk_shr(d1, 3 * (P - 4) + 1, 3 * (P - 4)));
+  } else if constexpr (P < 13) {
+    return mask_or<M, O>(pk_shr(d2, 3 * (P - 9) + 2, 3 * (P - 9) + 1));
+  } else if constexpr (P == 13) {
+    // c4: d0 bits 12..14 (low half); c31: d2 bits 29..31 (high half, relative 13)
+    return mask_or<M, O>(pk_shr((d0 & 0xFFFFu) | (d2 & 0xFFFF0000u), 12, 13));
+  } else if constexpr (P == 14) {
+    // c5: d0 bits 15..17; c26: d2 bits 14..16.  Bytes [d0.b1 d0.b2 | d2.b1 d2.b2] put them at 7 / 6.
+    return mask_or<M, O>(pk_shr(perm_b32(d2, d0, 0x06050201u), 7, 6));
+  } else {
+    // c10: stream bits 30..32; c21: stream bits 63..65.
+    const uint32_t c10 = __builtin_amdgcn_alignbit(d1, d0, 30);
+    const uint32_t c21 = __builtin_amdgcn_alignbit(d2, d1, 31);
+    return mask_or<M, O>(perm_b32(c21, c10, 0x05040100u));
+  }
+}
+
 template <bool MAGIC>
 __device__ __forceinline__ void unpack3(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t (&p)[16]) {
-  constexpr uint32_t M = 0x00070007u, O = MAGIC ? 0x64006400u : 0u;
-  p[0] = mask_or<M, O>(pk_shr(d0, 0, 2));
-  p[1] = mask_or<M, O>(pk_shr(d0, 3, 5));
-  p[2] = mask_or<M, O>(pk_shr(d0, 6, 8));
-  p[3] = mask_or<M, O>(pk_shr(d0, 9, 11));
-  p[4] = mask_or<M, O>(pk_shr(d1, 1, 0));
-  p[5] = mask_or<M, O>(pk_shr(d1, 4, 3));
-  p[6] = mask_or<M, O>(pk_shr(d1, 7, 6));
-  p[7] = mask_or<M, O>(pk_shr(d1, 10, 9));
-  p[8] = mask_or<M, O>(pk_shr(d1, 13, 12));
-  p[9] = mask_or<M, O>(pk_shr(d2, 2, 1));
-  p[10] = mask_or<M, O>(pk_shr(d2, 5, 4));
-  p[11] = mask_or<M, O>(pk_shr(d2, 8, 7));
-  p[12] = mask_or<M, O>(pk_shr(d2, 11, 10));
-  // c4: d0 bits 12..14 (low half); c31: d2 bits 29..31 (high half, relative 13)
-  p[13] = mask_or<M, O>(pk_shr((d0 & 0xFFFFu) | (d2 & 0xFFFF0000u), 12, 13));
-  // c5: d0 bits 15..17; c26: d2 bits 14..16.  Bytes [d0.b1 d0.b2 | d2.b1 d2.b2] put them at 7 / 6.
-  p[14] = mask_or<M, O>(pk_shr(perm_b32(d2, d0, 0x06050201u), 7, 6));
-  // c10: stream bits 30..32; c21: stream bits 63..65.
-  const uint32_t c10 = __builtin_amdgcn_alignbit(d1, d0, 30);
-  const uint32_t c21 = __builtin_amdgcn_alignbit(d2, d1, 31);
-  p[15] = mask_or<M, O>(perm_b32(c21, c10, 0x05040100u));
+  p[0] = pair3<0, MAGIC>(d0, d1, d2);
+  p[1] = pair3<1, MAGIC>(d0, d1, d2);
+  p[2] = pair3<2, MAGIC>(d0, d1, d2);
+  p[3] = pair3<3, MAGIC>(d0, d1, d2);
+  p[4] = pair3<4, MAGIC>(d0, d1, d2);
+  p[5] = pair3<5, MAGIC>(d0, d1, d2);
+  p[6] = pair3<6, MAGIC>(d0, d1, d2);
+  p[7] = pair3<7, MAGIC>(d0, d1, d2);
+  p[8] = pair3<8, MAGIC>(d0, d1, d2);
+  p[9] = pair3<9, MAGIC>(d0, d1, d2);
+  p[10] = pair3<10, MAGIC>(d0, d1, d2);
+  p[11] = pair3<11, MAGIC>(d0, d1, d2);
+  p[12] = pair3<12, MAGIC>(d0, d1, d2);
+  p[13] = pair3<13, MAGIC>(d0, d1, d2);
+  p[14] = pair3<14, MAGIC>(d0, d1, d2);
+  p[15] = pair3<15, MAGIC>(d0, d1, d2);
 }
 
 // 4-bit chunk (dwords d0..d3, nibble n of dword j = code 8j+n) -> 16 pairs.
@@ -124,6 +144,17 @@ __device__ __forceinline__ void unpack4(const uint32_t (&d)[4], uint32_t (&p)[16
   for (int j = 0; j < 4; ++j) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) p[4 * j + i] = mask_or<M, O>(d[j] >> (4 * i));
+  }
+}
+
+// Pair P of a chunk of either width.
+template <int BITS, int P, bool MAGIC>
+__device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&d)[4]) {
+  if constexpr (BITS == 3) {
+    return pair3<P, MAGIC>(d[0], d[1], d[2]);
+  } else {
+    constexpr uint32_t M = 0x000F000Fu, O = MAGIC ? 0x64006400u : 0u;
+    return mask_or<M, O>(d[P >> 2] >> (4 * (P & 3)));
   }
 }
 
@@ -315,6 +346,20 @@ __device__ __forceinline__ void buf_chunk(__amdgpu_buffer_rsrc_t r, uint32_t vof
 
 __device__ __forceinline__ uint16_t buf_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
+// One chunk of packed codes through a buffer resource with the default (cached) policy: the
+// grouped GEMMs read each expert's weights once per m-tile, so they are kept in L2.
+template <int BITS>
+__device__ __forceinline__ void buf_chunk_cached(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                                 uint32_t (&d)[4]) {
+  if constexpr (BITS == 3) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0);
+    d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = 0;
+  } else {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+  }
 }
 
 // Orderable key of a router logit: larger logit -> larger key, +0 == -0, NaN below all.

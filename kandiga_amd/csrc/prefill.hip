@@ -6,23 +6,16 @@
 // CPU calls).
 //
 //   xpair_kernel: x into pair order once per call (the k order the dequantized weights have).
-//   gemm_gateup_kernel: one workgroup per (m-tile of <= 128 sorted assignments of one
-//     expert, 64 intermediate columns).  Per 64-wide k step the workgroup gathers the
-//     tile's x rows (token = assignment / K, already in pair order) into LDS, dequantizes the 64
-//     gate rows and 64 up rows of that k step into LDS as fp16 (one quant group per row,
-//     round(q*s + b) by one fp16 fma), and runs v_mfma_f32_32x32x16_f16.  Each wave owns
-//     64 rows x 32 columns of both gate and up, so SwiGLU is applied in registers and
-//     act is written once (fp16, pair order for the down projection's k dimension).
-//     Every loader thread keeps two further k steps of global loads in flight in
-//     registers while the current step is multiplied out of LDS.
-//   gemm_down_kernel: one workgroup per (m-tile, 128 output columns); A = act rows of the
-//     tile (already contiguous and in pair order), B = dequantized down rows, same
-//     pipeline.  The output row of sorted position p is written, as fp16, to assignment
+//   gemm_gateup_kernel: one workgroup per (m-tile of <= 128 sorted assignments of one expert,
+//     256 intermediate columns of both gate and up); SwiGLU in registers, act written once
+//     (fp16, pair order for the down projection's k dimension).
+//   gemm_down_kernel: one workgroup per (m-tile, 512 output columns); A = act rows of the tile
+//     (contiguous, pair order).  The output row of sorted position p is written to assignment
 //     perm[p]: fp16 for the switch_mlp contract, or fp32 scaled by that assignment's routing
 //     weight for the fused layer (an fp16 intermediate would add up to half an fp16 ulp of
-//     each term before the combine, which the 2e-2 bound cannot absorb when terms cancel).
-//   Tiles are ordered so that the column tiles of one m-tile, and the m-tiles of one
-//   expert, run on the same XCD and share its L2.
+//     each term before the combine).
+//   Both run v_mfma_f32_32x32x16_f16 with the weights dequantized in registers (see the grouped
+//   GEMM section below).
 //   combine_kernel: out[t] = sum_k w[t,k] * y[t,k] (+ shared expert), fp32 accumulate in
 //     k order, one rounding to the output type (moe_block.metal:515-539).
 #include "kmoe_device.h"
@@ -61,9 +54,6 @@ __device__ __forceinline__ float activate_p(float g, float u) {
   }
 }
 
-constexpr int BK = 64;   // k step = one quantization group
-constexpr int LDH = 72;  // LDS row stride in halves (64 + 8 pad: 144 bytes)
-
 __device__ __forceinline__ void load16g(const void* p, uint32_t (&v)[16]) {
   const uint4* s = reinterpret_cast<const uint4*>(p);
 #pragma unroll
@@ -82,53 +72,9 @@ __device__ __forceinline__ void store16s(_Float16* dst, const uint32_t (&v)[16])
   for (int q = 0; q < 4; ++q) d[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
 }
 
-// Load one chunk of packed codes through the caches (weights of one expert are read by every
-// m-tile of that expert, so prefill keeps them in L2; decode streams them nontemporally).
-template <int BITS>
-__device__ __forceinline__ void load_chunk_c(const uint8_t* __restrict__ row, int chunk, uint32_t (&d)[4]) {
-  const uint32_t* src = reinterpret_cast<const uint32_t*>(row + (size_t)chunk * Bits<BITS>::chunk_bytes);
-  if constexpr (BITS == 3) {
-    d[0] = src[0];
-    d[1] = src[1];
-    d[2] = src[2];
-    d[3] = 0;
-  } else {
-    const uint4 v = *reinterpret_cast<const uint4*>(src);
-    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-  }
-}
-
-// Dequantize loaded codes of one 32-code chunk into 16 fp16 pairs (pair order).
-template <int BITS, bool BF16>
-__device__ __forceinline__ void dequant_regs(const uint32_t (&d)[4], uint16_t sbits, uint16_t bbits,
-                                             uint32_t (&out)[16]) {
-  const float sf = scale_to_f32<BF16>(sbits), bf = scale_to_f32<BF16>(bbits);
-  const half2_t s2 = {(_Float16)sf, (_Float16)sf}, b2 = {(_Float16)bf, (_Float16)bf};
-  unpack_chunk<BITS, true>(d, out);
-#pragma unroll
-  for (int p = 0; p < 16; ++p) out[p] = dequant_pair(out[p], s2, b2);
-}
-
 __device__ __forceinline__ float16_t mfma32(const half8_t a, const half8_t b, const float16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
-
-// Tile index (m-tile * ncol + column tile) of workgroup b.  Workgroups are dealt to the 8 XCDs
-// round-robin (XCD x runs b = x, x+8, ...); XCD x takes m-tiles x, x+8, ... and runs all column
-// tiles of one m-tile back to back, so the gathered rows of an m-tile are fetched into one L2
-// and the valid m-tiles (a prefix of the grid) are spread evenly over the XCDs.  The grid
-// holds a multiple of 8 m-tiles.
-__device__ __forceinline__ int xcd_tile(int b, int ncol) {
-  const int x = b & 7, j = b >> 3;
-  return ((j / ncol) * 8 + x) * ncol + (j % ncol);
-}
-
-// Registers of one k step (64 wide) of one loader thread: an A chunk and a B chunk.
-struct KStage {
-  uint32_t a[16];
-  uint32_t w[4];
-  uint16_t s, b;
-};
 
 // x [T][H] -> pair order within each 32-wide chunk (the k order of the dequantized weights).
 template <int BITS>
@@ -142,115 +88,289 @@ __global__ __launch_bounds__(256) void xpair_kernel(const uint16_t* __restrict__
   store16s(reinterpret_cast<_Float16*>(xpp + c * CHUNK), pr);
 }
 
+// ---- grouped GEMMs ----------------------------------------------------------------------
+// Shared structure of both GEMMs.  A workgroup (4 waves) owns one m-tile: up to GEMM_BM = 128
+// expert-sorted assignment rows of one expert, as four 32-row blocks.  Each wave owns two
+// 32-column blocks of the output for all of the tile's rows, so its 8 accumulator blocks of
+// v_mfma_f32_32x32x16_f16 hold 128 x 64 fp32 values, and two workgroups fit on a CU: while one
+// waits at its k-step barrier or for loads, the other's waves issue.
+//
+//   * A (x rows for gate/up, act rows for down) is shared by the four waves: per 64-wide k step
+//     (one quantization group) the tile's rows are loaded once into an LDS slab (double
+//     buffered, one barrier per k step).  Rows are already in pair order, the k order in which
+//     the weight codes unpack.
+//   * B (the weights) never goes through LDS: no other wave needs a wave's columns, so each
+//     lane dequantizes its own fragments in registers.  Lane (n, h) = (lane & 31, lane >> 5)
+//     of a column block holds weight row n; for one quantization group it loads code chunk h
+//     (codes 32h..32h+31, 12 or 16 bytes) and that row's scale and bias, and the four k16
+//     steps of the group take pairs 4s..4s+3 of the chunk as their 8 fp16 values: exactly the
+//     MFMA B layout (k = 8h..8h+7 of each step), with the A fragment read at the same pair-order
+//     positions.  round(q*s + b) is one packed subtract and one packed fma per two weights.
+//   * Only the 32-row blocks that hold assignments are multiplied (the kernel body is
+//     instantiated for 1..4 blocks), so a ragged expert costs its rows rounded up to 32, not
+//     to 128.
+//   * Weights and scales come through per-projection buffer resources, so a weight row past
+//     the projection's end reads zeros (such columns are computed but never stored).
+// The codes of the group after next and the A rows of the next group are loaded while a group
+// is multiplied.
+
+constexpr int LDA = 72;                      // halves per row of the A slab (64 + 8 pad: 144 B)
+constexpr int SLAB = GEMM_BM * LDA;          // halves per slab buffer
+
+// Workgroup b -> (m-tile, column tile).  Workgroups are dealt to the 8 XCDs round-robin (XCD x
+// runs b = x, x+8, ...).  XCD x takes a contiguous share of the m-tile list (the m-tiles of one
+// expert are consecutive there, so the expert's weights stay in that XCD's L2) and runs the
+// column tiles of one m-tile back to back (they share its A rows).  The grid holds
+// 8 * ceil(max_mtiles / 8) * ncol workgroups; the actual count nmt is read on the device.
+__device__ __forceinline__ bool xcd_mtile(int b, int ncol, int nmt, int& mt, int& ct) {
+  const int x = b & 7, j = b >> 3;
+  const int lm = j / ncol;
+  ct = j - lm * ncol;
+  const int share = (nmt + 7) >> 3;
+  mt = x * share + lm;
+  return lm < share && mt < nmt;
+}
+
+// A value every lane of the wave holds, moved to a scalar register (buffer resources and
+// branches built from it stay uniform).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// One quantization group of a lane's JB weight rows.
+template <int JB>
+struct BGroup {
+  uint32_t d[JB][4];
+  uint16_t s[JB], b[JB];
+};
+
+// Weight rows of a lane: row j's codes/scales/biases through resources rw/rs/rb[j] at lane
+// offsets vw/vs[j] (bytes).  Group g adds the uniform offsets 2g chunks / 2g bytes.
+template <int JB>
+struct BRows {
+  __amdgpu_buffer_rsrc_t rw[JB], rs[JB], rb[JB];
+  uint32_t vw[JB], vs[JB];
+};
+
+template <int BITS, int JB>
+__device__ __forceinline__ void load_group(const BRows<JB>& R, int g, BGroup<JB>& G) {
+  const uint32_t sw = (uint32_t)uniform(g * 2 * Bits<BITS>::chunk_bytes), ss = (uint32_t)uniform(g * 2);
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    buf_chunk_cached<BITS>(R.rw[j], R.vw[j], sw, G.d[j]);
+    G.s[j] = buf_u16(R.rs[j], R.vs[j], ss);
+    G.b[j] = buf_u16(R.rb[j], R.vs[j], ss);
+  }
+}
+
+// k16 step ST of one group: A fragments of the NB active row blocks from the slab, B fragments
+// of the JB column blocks dequantized from the group's codes.
+template <int BITS, int NB, int JB, int ST>
+__device__ __forceinline__ void gemm_step(float16_t (&acc)[4][JB], const _Float16* __restrict__ slab, int lane,
+                                          const BGroup<JB>& G, const half2_t (&s2)[JB], const half2_t (&b2)[JB]) {
+  const _Float16* ap = slab + (lane & 31) * LDA + 32 * (lane >> 5) + 8 * ST;
+  half8_t af[NB];
+#pragma unroll
+  for (int mb = 0; mb < NB; ++mb) af[mb] = *reinterpret_cast<const half8_t*>(ap + 32 * mb * LDA);
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    const u32x4_t q = {dequant_pair(chunk_pair<BITS, 4 * ST + 0, true>(G.d[j]), s2[j], b2[j]),
+                       dequant_pair(chunk_pair<BITS, 4 * ST + 1, true>(G.d[j]), s2[j], b2[j]),
+                       dequant_pair(chunk_pair<BITS, 4 * ST + 2, true>(G.d[j]), s2[j], b2[j]),
+                       dequant_pair(chunk_pair<BITS, 4 * ST + 3, true>(G.d[j]), s2[j], b2[j])};
+    const half8_t bf = __builtin_bit_cast(half8_t, q);
+#pragma unroll
+    for (int mb = 0; mb < NB; ++mb) acc[mb][j] = mfma32(af[mb], bf, acc[mb][j]);
+  }
+}
+
+template <int BITS, bool BF16, int NB, int JB>
+__device__ __forceinline__ void gemm_group(float16_t (&acc)[4][JB], const _Float16* __restrict__ slab, int lane,
+                                           const BGroup<JB>& G) {
+  half2_t s2[JB], b2[JB];
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    const _Float16 sf = (_Float16)scale_to_f32<BF16>(G.s[j]), bf = (_Float16)scale_to_f32<BF16>(G.b[j]);
+    s2[j] = (half2_t){sf, sf};
+    b2[j] = (half2_t){bf, bf};
+  }
+  gemm_step<BITS, NB, JB, 0>(acc, slab, lane, G, s2, b2);
+  gemm_step<BITS, NB, JB, 1>(acc, slab, lane, G, s2, b2);
+  gemm_step<BITS, NB, JB, 2>(acc, slab, lane, G, s2, b2);
+  gemm_step<BITS, NB, JB, 3>(acc, slab, lane, G, s2, b2);
+}
+
+// Workgroup barrier for the LDS slabs only: waits for this wave's LDS writes, not for its
+// global loads, so the prefetched groups stay in flight across it (__syncthreads would wait for
+// every outstanding load).  The memory clobber keeps the compiler from moving LDS accesses
+// across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// The k loop over ng groups.  Thread t stages half (t & 1) of slab row t >> 1 from arow (a row
+// of ng*64 halves).  Every load is unconditional (past the last group the index is clamped,
+// re-reading that group), so the wait counts before each use are exact.
+template <int BITS, bool BF16, int NB, int JB>
+__device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16* __restrict__ sA,
+                                              const uint16_t* __restrict__ arow, const BRows<JB>& R, int ng) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  _Float16* const st = sA + (tid >> 1) * LDA + 32 * (tid & 1);
+  const uint16_t* const ag = arow + 32 * (tid & 1);
+  const int last = ng - 1;
+  uint32_t ar[16];
+  BGroup<JB> G0, G1;
+  load_group<BITS>(R, 0, G0);
+  load_group<BITS>(R, min(1, last), G1);
+  load16g(ag, ar);
+  store16s(st, ar);
+  load16g(ag + (size_t)min(1, last) * 64, ar);
+  lds_barrier();
+  // pairs of groups (slab 0, then slab 1), so the loop has one exit; an odd last group follows
+  int g = 0;
+  for (; g + 1 < ng; g += 2) {
+    gemm_group<BITS, BF16, NB>(acc, sA, lane, G0);
+    load_group<BITS>(R, min(g + 2, last), G0);
+    store16s(st + SLAB, ar);
+    load16g(ag + (size_t)min(g + 2, last) * 64, ar);
+    lds_barrier();
+    gemm_group<BITS, BF16, NB>(acc, sA + SLAB, lane, G1);
+    load_group<BITS>(R, min(g + 3, last), G1);
+    store16s(st, ar);
+    load16g(ag + (size_t)min(g + 3, last) * 64, ar);
+    lds_barrier();
+  }
+  if (g < ng) gemm_group<BITS, BF16, NB>(acc, sA, lane, G0);
+}
+
+template <int JB>
+__device__ __forceinline__ void zero_acc(float16_t (&acc)[4][JB]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
+}
+
+// Columns per workgroup: gate/up waves own 32 intermediate columns of both gate and up (column
+// block 0 = gate rows c0 + n, block 1 = the same up rows); down waves own 64 output columns.
+constexpr int GU_COLS = 4 * 32;  // intermediate columns per gate/up workgroup
+constexpr int DN_COLS = 4 * 64;  // output columns per down workgroup
+
+// gate/up GEMM + SwiGLU.  Column tile ct covers intermediate columns [128ct, 128ct + 128); wave w
+// the 32 columns c0 = 128ct + 32w + n.  Each lane holds matching gate and up values and writes
+// act = silu(gate) * up (fp16, pair order within each 32-column chunk, the down projection's k
+// order) for the sorted position of each row.
+template <int BITS, bool BF16, int ACT, int NB>
+__device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* __restrict__ x, int K,
+                                            const int32_t* __restrict__ perm, int e, int row0, int nrows, int ct,
+                                            _Float16* sA, uint16_t* __restrict__ act) {
+  const int H = L.H, I = L.I;
+  const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
+  const int lr = tid >> 1;
+  const int tok = perm[row0 + min(lr, nrows - 1)] / K;  // rows past the tile's end reload its last row
+  const int c0 = ct * GU_COLS + wave * 32;
+  const uint32_t rbytes = (uint32_t)H * BITS / 8, ng = (uint32_t)H / GROUP;
+  BRows<2> R;
+  const uint32_t row = (uint32_t)(c0 + (lane & 31));
+  R.rw[0] = make_rsrc(L.gate.w + (size_t)e * L.gate.w_stride, (uint32_t)I * rbytes);
+  R.rw[1] = make_rsrc(L.up.w + (size_t)e * L.up.w_stride, (uint32_t)I * rbytes);
+  R.rs[0] = make_rsrc(L.gate.s + (size_t)e * L.gate.s_stride, (uint32_t)I * ng * 2u);
+  R.rb[0] = make_rsrc(L.gate.b + (size_t)e * L.gate.s_stride, (uint32_t)I * ng * 2u);
+  R.rs[1] = make_rsrc(L.up.s + (size_t)e * L.up.s_stride, (uint32_t)I * ng * 2u);
+  R.rb[1] = make_rsrc(L.up.b + (size_t)e * L.up.s_stride, (uint32_t)I * ng * 2u);
+  R.vw[0] = R.vw[1] = row * rbytes + (uint32_t)(lane >> 5) * Bits<BITS>::chunk_bytes;
+  R.vs[0] = R.vs[1] = row * ng * 2u;
+  float16_t acc[4][2];
+  zero_acc(acc);
+  gemm_mainloop<BITS, BF16, NB>(acc, sA, x + (size_t)tok * H, R, (int)ng);
+  if (c0 >= I) return;
+  const int h = lane >> 5;
+  uint16_t* const ap = act + (size_t)row0 * I + c0 + pairpos_p<BITS>(lane & 31);
+#pragma unroll
+  for (int mb = 0; mb < NB; ++mb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int r = 32 * mb + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (r < nrows) ap[(size_t)r * I] = f32_to_f16_bits(activate_p<ACT>(acc[mb][0][v], acc[mb][1][v]));
+    }
+  }
+}
+
 template <int BITS, bool BF16, int ACT>
-__global__ __launch_bounds__(256, 3) void gemm_gateup_kernel(const LayerArgs L, const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(256, 2) void gemm_gateup_kernel(const LayerArgs L, const uint16_t* __restrict__ x,
                                                              int K, const int32_t* __restrict__ perm,
                                                              const int32_t* __restrict__ scalars,
                                                              const int32_t* __restrict__ mt_expert,
                                                              const int32_t* __restrict__ mt_row0,
                                                              const int32_t* __restrict__ mt_rows,
                                                              uint16_t* __restrict__ act) {
-  constexpr int BNI = 64;  // intermediate columns per tile (gate and up each)
-  __shared__ __attribute__((aligned(16))) _Float16 sA[GEMM_BM * LDH];
-  __shared__ __attribute__((aligned(16))) _Float16 sB[2 * BNI * LDH];
-  const int H = L.H, I = L.I;
-  const int n_it = I / BNI;
-  const int q = xcd_tile(blockIdx.x, n_it);
-  const int mt = q / n_it, it = q - mt * n_it;
-  if (mt >= scalars[1]) return;
-  const int e = mt_expert[mt], row0 = mt_row0[mt], nrows = mt_rows[mt];
-  const int i0 = it * BNI;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  const int lr = tid >> 1, lc = tid & 1;  // loader: tile row 0..127, chunk 0..1 of the k step
-  const bool a_ok = lr < nrows;
-  const int tok = a_ok ? perm[row0 + lr] / K : 0;
-  const uint16_t* xrow = x + (size_t)tok * H;
-  const bool is_up = lr >= BNI;
-  const uint8_t* wbase = is_up ? L.up.w : L.gate.w;
-  const uint16_t* sbase = is_up ? L.up.s : L.gate.s;
-  const uint16_t* bbase = is_up ? L.up.b : L.gate.b;
-  const int64_t wst = is_up ? L.up.w_stride : L.gate.w_stride;
-  const int64_t sst = is_up ? L.up.s_stride : L.gate.s_stride;
-  const int brow = i0 + (lr & (BNI - 1));
-  const size_t rbytes = (size_t)H * BITS / 8;
-  const int ng = H / GROUP;
-  const uint8_t* wrow = wbase + (size_t)e * wst + (size_t)brow * rbytes;
-  const uint16_t* srow = sbase + (size_t)e * sst + (size_t)brow * ng;
-  const uint16_t* bsrow = bbase + (size_t)e * sst + (size_t)brow * ng;
-
-  float16_t acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int qq = 0; qq < 16; ++qq) acc[i][j][qq] = 0.f;
-
-  // rows past the end of the tile read token 0's x (their results are never stored)
-  auto load = [&](KStage& S, int k0) {
-    load16g(xrow + k0 + lc * CHUNK, S.a);
-    load_chunk_c<BITS>(wrow, (k0 >> 5) + lc, S.w);
-    S.s = srow[k0 >> 6];
-    S.b = bsrow[k0 >> 6];
-  };
-  auto store = [&](const KStage& S) {
-    uint32_t pb[16];
-    dequant_regs<BITS, BF16>(S.w, S.s, S.b, pb);
-    store16s(sA + lr * LDH + lc * CHUNK, S.a);
-    store16s(sB + lr * LDH + lc * CHUNK, pb);
-  };
-  auto mma = [&]() {
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int koff = ks * 16 + (lane >> 5) * 8;
-      const half8_t a0 = *reinterpret_cast<const half8_t*>(sA + (64 * wm + (lane & 31)) * LDH + koff);
-      const half8_t a1 = *reinterpret_cast<const half8_t*>(sA + (64 * wm + 32 + (lane & 31)) * LDH + koff);
-      const half8_t bg = *reinterpret_cast<const half8_t*>(sB + (32 * wn + (lane & 31)) * LDH + koff);
-      const half8_t bu = *reinterpret_cast<const half8_t*>(sB + (BNI + 32 * wn + (lane & 31)) * LDH + koff);
-      acc[0][0] = mfma32(a0, bg, acc[0][0]);
-      acc[0][1] = mfma32(a0, bu, acc[0][1]);
-      acc[1][0] = mfma32(a1, bg, acc[1][0]);
-      acc[1][1] = mfma32(a1, bu, acc[1][1]);
-    }
-  };
-  // two k steps of loads in flight: while step k is multiplied out of LDS, the registers of
-  // steps k+1 and k+2 are being filled (unrolled by two so no stage register is copied)
-  const int nk = H / BK;
-  KStage S0, S1;
-  load(S0, 0);
-  if (nk > 1) load(S1, BK);
-  for (int kk = 0; kk < nk; kk += 2) {
-    store(S0);
-    __syncthreads();
-    if (kk + 2 < nk) load(S0, (kk + 2) * BK);
-    mma();
-    __syncthreads();
-    if (kk + 1 < nk) {
-      store(S1);
-      __syncthreads();
-      if (kk + 3 < nk) load(S1, (kk + 3) * BK);
-      mma();
-      __syncthreads();
-    }
+  __shared__ __attribute__((aligned(16))) _Float16 sA[2 * SLAB];
+  int mt, ct;
+  if (!xcd_mtile(blockIdx.x, (L.I + GU_COLS - 1) / GU_COLS, uniform(scalars[1]), mt, ct)) return;
+  const int e = uniform(mt_expert[mt]), row0 = uniform(mt_row0[mt]), nrows = uniform(mt_rows[mt]);
+  switch ((nrows + 31) >> 5) {
+    case 1: gateup_tile<BITS, BF16, ACT, 1>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    case 2: gateup_tile<BITS, BF16, ACT, 2>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    case 3: gateup_tile<BITS, BF16, ACT, 3>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    default: gateup_tile<BITS, BF16, ACT, 4>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
   }
-  const int col = lane & 31;
-  const int cbase = i0 + 32 * wn;
-  const int cpos = pairpos_p<BITS>(col);
+}
+
+// down GEMM.  Column tile ct covers output columns [256ct, 256ct + 256); wave w the 64 columns
+// c0 + 32j + n with c0 = 256ct + 64w (j = 0, 1).  Row r of the tile (sorted position row0 + r)
+// is written to its assignment perm[row0 + r]: fp16 unweighted (the switch_mlp contract) or fp32
+// scaled by the assignment's routing weight (the fused layer, summed by combine_kernel).
+template <int BITS, bool BF16, bool OUT16, int NB>
+__device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, int nrows, int ct, _Float16* sA,
+                                          const int32_t* s_asg, const float* s_wa,
+                                          const uint16_t* __restrict__ act, float* __restrict__ y32,
+                                          uint16_t* __restrict__ y16) {
+  const int H = L.H, I = L.I;
+  const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
+  const int lr = tid >> 1;
+  const int c0 = ct * DN_COLS + wave * 64;
+  const uint32_t rbytes = (uint32_t)I * BITS / 8, ng = (uint32_t)I / GROUP;
+  BRows<2> R;
+  const auto dw = make_rsrc(L.down.w + (size_t)e * L.down.w_stride, (uint32_t)H * rbytes);
+  const auto ds = make_rsrc(L.down.s + (size_t)e * L.down.s_stride, (uint32_t)H * ng * 2u);
+  const auto db = make_rsrc(L.down.b + (size_t)e * L.down.s_stride, (uint32_t)H * ng * 2u);
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t row = (uint32_t)(c0 + 32 * j + (lane & 31));
+    R.rw[j] = dw;
+    R.rs[j] = ds;
+    R.rb[j] = db;
+    R.vw[j] = row * rbytes + (uint32_t)(lane >> 5) * Bits<BITS>::chunk_bytes;
+    R.vs[j] = row * ng * 2u;
+  }
+  float16_t acc[4][2];
+  zero_acc(acc);
+  gemm_mainloop<BITS, BF16, NB>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, R, (int)ng);
+  const int h = lane >> 5;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int r = 64 * wm + 32 * mb + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
-      if (r < nrows)
-        act[(size_t)(row0 + r) * I + cbase + cpos] = f32_to_f16_bits(activate_p<ACT>(acc[mb][0][j], acc[mb][1][j]));
+  for (int mb = 0; mb < NB; ++mb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int r = 32 * mb + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (r < nrows) {
+        const size_t ybase = (size_t)s_asg[r] * H;
+        const float wa = s_wa[r];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int cb = c0 + 32 * j;
+          if (cb < H) {
+            if constexpr (OUT16) {
+              y16[ybase + cb + (lane & 31)] = f32_to_f16_bits(acc[mb][j][v] * wa);
+            } else {
+              y32[ybase + cb + (lane & 31)] = acc[mb][j][v] * wa;
+            }
+          }
+        }
+      }
     }
   }
 }
 
 template <int BITS, bool BF16, bool OUT16>
-__global__ __launch_bounds__(256, 3) void gemm_down_kernel(const LayerArgs L, const int32_t* __restrict__ perm,
+__global__ __launch_bounds__(256, 2) void gemm_down_kernel(const LayerArgs L, const int32_t* __restrict__ perm,
                                                            const int32_t* __restrict__ scalars,
                                                            const int32_t* __restrict__ mt_expert,
                                                            const int32_t* __restrict__ mt_row0,
@@ -258,117 +378,23 @@ __global__ __launch_bounds__(256, 3) void gemm_down_kernel(const LayerArgs L, co
                                                            const uint16_t* __restrict__ act,
                                                            const float* __restrict__ wscale,
                                                            float* __restrict__ y32, uint16_t* __restrict__ y16) {
-  constexpr int BN = 128;
-  __shared__ __attribute__((aligned(16))) _Float16 sA[GEMM_BM * LDH];
-  __shared__ __attribute__((aligned(16))) _Float16 sB[BN * LDH];
+  __shared__ __attribute__((aligned(16))) _Float16 sA[2 * SLAB];
   __shared__ int32_t s_asg[GEMM_BM];  // assignment of each tile row, and its routing weight
   __shared__ float s_wa[GEMM_BM];
-  const int H = L.H, I = L.I;
-  const int n_ht = (H + BN - 1) / BN;
-  const int q = xcd_tile(blockIdx.x, n_ht);
-  const int mt = q / n_ht, ht = q - mt * n_ht;
-  if (mt >= scalars[1]) return;
-  const int e = mt_expert[mt], row0 = mt_row0[mt], nrows = mt_rows[mt];
-  const int h0 = ht * BN;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  const int lr = tid >> 1, lc = tid & 1;
-  const bool a_ok = lr < nrows;
-  const uint16_t* arow = act + (size_t)(row0 + (a_ok ? lr : 0)) * I;
-  if (tid < GEMM_BM) {  // epilogue metadata, fetched while the k loop runs (read after its barriers)
+  int mt, ct;
+  if (!xcd_mtile(blockIdx.x, (L.H + DN_COLS - 1) / DN_COLS, uniform(scalars[1]), mt, ct)) return;
+  const int e = uniform(mt_expert[mt]), row0 = uniform(mt_row0[mt]), nrows = uniform(mt_rows[mt]);
+  const int tid = threadIdx.x;
+  if (tid < GEMM_BM) {  // read after the k loop's barriers
     const int a = tid < nrows ? perm[row0 + tid] : 0;
     s_asg[tid] = a;
     s_wa[tid] = wscale && tid < nrows ? wscale[a] : 1.0f;
   }
-  const int brow = h0 + lr;
-  const bool b_ok = brow < H;
-  const size_t rbytes = (size_t)I * BITS / 8;
-  const int ng = I / GROUP;
-  const int brow_c = b_ok ? brow : 0;
-  const uint8_t* wrow = L.down.w + (size_t)e * L.down.w_stride + (size_t)brow_c * rbytes;
-  const uint16_t* srow = L.down.s + (size_t)e * L.down.s_stride + (size_t)brow_c * ng;
-  const uint16_t* bsrow = L.down.b + (size_t)e * L.down.s_stride + (size_t)brow_c * ng;
-
-  float16_t acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int qq = 0; qq < 16; ++qq) acc[i][j][qq] = 0.f;
-
-  // rows past the end of the tile read the tile's first act row (their results are never stored)
-  auto load = [&](KStage& S, int k0) {
-    load16g(arow + k0 + lc * CHUNK, S.a);
-    load_chunk_c<BITS>(wrow, (k0 >> 5) + lc, S.w);
-    S.s = srow[k0 >> 6];
-    S.b = bsrow[k0 >> 6];
-  };
-  auto store = [&](const KStage& S) {
-    uint32_t pb[16];
-    if (b_ok) {
-      dequant_regs<BITS, BF16>(S.w, S.s, S.b, pb);
-    } else {
-#pragma unroll
-      for (int qq = 0; qq < 16; ++qq) pb[qq] = 0u;
-    }
-    store16s(sA + lr * LDH + lc * CHUNK, S.a);
-    store16s(sB + lr * LDH + lc * CHUNK, pb);
-  };
-  auto mma = [&]() {
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int koff = ks * 16 + (lane >> 5) * 8;
-      const half8_t a0 = *reinterpret_cast<const half8_t*>(sA + (64 * wm + (lane & 31)) * LDH + koff);
-      const half8_t a1 = *reinterpret_cast<const half8_t*>(sA + (64 * wm + 32 + (lane & 31)) * LDH + koff);
-      const half8_t b0 = *reinterpret_cast<const half8_t*>(sB + (64 * wn + (lane & 31)) * LDH + koff);
-      const half8_t b1 = *reinterpret_cast<const half8_t*>(sB + (64 * wn + 32 + (lane & 31)) * LDH + koff);
-      acc[0][0] = mfma32(a0, b0, acc[0][0]);
-      acc[0][1] = mfma32(a0, b1, acc[0][1]);
-      acc[1][0] = mfma32(a1, b0, acc[1][0]);
-      acc[1][1] = mfma32(a1, b1, acc[1][1]);
-    }
-  };
-  const int nk = I / BK;
-  KStage S0, S1;
-  load(S0, 0);
-  if (nk > 1) load(S1, BK);
-  for (int kk = 0; kk < nk; kk += 2) {
-    store(S0);
-    __syncthreads();
-    if (kk + 2 < nk) load(S0, (kk + 2) * BK);
-    mma();
-    __syncthreads();
-    if (kk + 1 < nk) {
-      store(S1);
-      __syncthreads();
-      if (kk + 3 < nk) load(S1, (kk + 3) * BK);
-      mma();
-      __syncthreads();
-    }
-  }
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int r = 64 * wm + 32 * mb + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
-      if (r < nrows) {
-        const size_t ybase = (size_t)s_asg[r] * H;
-        const float wa = s_wa[r];
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const int h = h0 + 64 * wn + 32 * nb + (lane & 31);
-          if (h < H) {
-            if constexpr (OUT16) {
-              y16[ybase + h] = f32_to_f16_bits(acc[mb][nb][j] * wa);
-            } else {
-              y32[ybase + h] = acc[mb][nb][j] * wa;
-            }
-          }
-        }
-      }
-    }
+  switch ((nrows + 31) >> 5) {
+    case 1: down_tile<BITS, BF16, OUT16, 1>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    case 2: down_tile<BITS, BF16, OUT16, 2>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    case 3: down_tile<BITS, BF16, OUT16, 3>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    default: down_tile<BITS, BF16, OUT16, 4>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
   }
 }
 
@@ -421,19 +447,18 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
                             uint16_t* y16, const float* wscale, hipStream_t s) {
   const LayerArgs& L = c.args;
   (void)T;
-  const int gmt = (max_mtiles + 7) & ~7;  // m-tiles of the grid: a multiple of 8 (see xcd_tile)
-  KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT>), dim3(gmt * (L.I / 64)), dim3(256),
-              0, s, L, x, c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act);
+  const int per_xcd = (max_mtiles + 7) / 8;  // m-tiles of one XCD's share at most (see xcd_mtile)
+  KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT>), dim3(8 * per_xcd * ((L.I + GU_COLS - 1) / GU_COLS)),
+              dim3(256), 0, s, L, x, c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  const int n_ht = (L.H + 127) / 128;
+  const dim3 grid_down(8 * per_xcd * ((L.H + DN_COLS - 1) / DN_COLS));
   if (y16) {
-    KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, true>), dim3(gmt * n_ht), dim3(256), 0, s,
-                L, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale,
-                (float*)nullptr, y16);
+    KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, true>), grid_down, dim3(256), 0, s, L, w.perm,
+                w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale, (float*)nullptr, y16);
   } else {
-    KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, false>), dim3(gmt * n_ht), dim3(256), 0, s,
-                L, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale, w.y32,
+    KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, false>), grid_down, dim3(256), 0, s, L, w.perm,
+                w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale, w.y32,
                 (uint16_t*)nullptr);
   }
   return hipGetLastError();
