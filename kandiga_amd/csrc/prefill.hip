@@ -135,11 +135,19 @@ __device__ __forceinline__ bool xcd_mtile(int b, int ncol, int nmt, int& mt, int
 // branches built from it stay uniform).
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// One quantization group of a lane's JB weight rows.
+// One quantization group of a lane's JB weight rows: codes and (per-group scale path) the
+// row's scale and bias.
 template <int JB>
 struct BGroup {
   uint32_t d[JB][4];
   uint16_t s[JB], b[JB];
+};
+
+// Scales and biases of two consecutive groups (2p: low half, 2p+1: high half) of a lane's rows,
+// one 4-byte load each; used when a row holds an even number of groups (4-byte aligned rows).
+template <int JB>
+struct BScalePair {
+  uint32_t s[JB], b[JB];
 };
 
 // Weight rows of a lane: row j's codes/scales/biases through resources rw/rs/rb[j] at lane
@@ -150,14 +158,26 @@ struct BRows {
   uint32_t vw[JB], vs[JB];
 };
 
-template <int BITS, int JB>
+template <int BITS, int JB, bool SCALES>
 __device__ __forceinline__ void load_group(const BRows<JB>& R, int g, BGroup<JB>& G) {
   const uint32_t sw = (uint32_t)uniform(g * 2 * Bits<BITS>::chunk_bytes), ss = (uint32_t)uniform(g * 2);
 #pragma unroll
   for (int j = 0; j < JB; ++j) {
     buf_chunk_cached<BITS>(R.rw[j], R.vw[j], sw, G.d[j]);
-    G.s[j] = buf_u16(R.rs[j], R.vs[j], ss);
-    G.b[j] = buf_u16(R.rb[j], R.vs[j], ss);
+    if constexpr (SCALES) {
+      G.s[j] = buf_u16(R.rs[j], R.vs[j], ss);
+      G.b[j] = buf_u16(R.rb[j], R.vs[j], ss);
+    }
+  }
+}
+
+template <int JB>
+__device__ __forceinline__ void load_scale_pair(const BRows<JB>& R, int p, BScalePair<JB>& S) {
+  const uint32_t ss = (uint32_t)uniform(p * 4);
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    S.s[j] = __builtin_amdgcn_raw_buffer_load_b32(R.rs[j], R.vs[j], ss, 0);
+    S.b[j] = __builtin_amdgcn_raw_buffer_load_b32(R.rb[j], R.vs[j], ss, 0);
   }
 }
 
@@ -182,13 +202,14 @@ __device__ __forceinline__ void gemm_step(float16_t (&acc)[4][JB], const _Float1
   }
 }
 
+// One group: sc/bi are the rows' scale and bias bits.
 template <int BITS, bool BF16, int NB, int JB>
 __device__ __forceinline__ void gemm_group(float16_t (&acc)[4][JB], const _Float16* __restrict__ slab, int lane,
-                                           const BGroup<JB>& G) {
+                                           const BGroup<JB>& G, const uint16_t (&sc)[JB], const uint16_t (&bi)[JB]) {
   half2_t s2[JB], b2[JB];
 #pragma unroll
   for (int j = 0; j < JB; ++j) {
-    const _Float16 sf = (_Float16)scale_to_f32<BF16>(G.s[j]), bf = (_Float16)scale_to_f32<BF16>(G.b[j]);
+    const _Float16 sf = (_Float16)scale_to_f32<BF16>(sc[j]), bf = (_Float16)scale_to_f32<BF16>(bi[j]);
     s2[j] = (half2_t){sf, sf};
     b2[j] = (half2_t){bf, bf};
   }
@@ -196,6 +217,15 @@ __device__ __forceinline__ void gemm_group(float16_t (&acc)[4][JB], const _Float
   gemm_step<BITS, NB, JB, 1>(acc, slab, lane, G, s2, b2);
   gemm_step<BITS, NB, JB, 2>(acc, slab, lane, G, s2, b2);
   gemm_step<BITS, NB, JB, 3>(acc, slab, lane, G, s2, b2);
+}
+
+template <int JB>
+__device__ __forceinline__ void pair_half(const BScalePair<JB>& S, int hi, uint16_t (&sc)[JB], uint16_t (&bi)[JB]) {
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    sc[j] = (uint16_t)(hi ? S.s[j] >> 16 : S.s[j] & 0xFFFFu);
+    bi[j] = (uint16_t)(hi ? S.b[j] >> 16 : S.b[j] & 0xFFFFu);
+  }
 }
 
 // Workgroup barrier for the LDS slabs only: waits for this wave's LDS writes, not for its
@@ -206,8 +236,9 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 // The k loop over ng groups.  Thread t stages half (t & 1) of slab row t >> 1 from arow (a row
 // of ng*64 halves).  Every load is unconditional (past the last group the index is clamped,
-// re-reading that group), so the wait counts before each use are exact.
-template <int BITS, bool BF16, int NB, int JB>
+// re-reading that group), so the wait counts before each use are exact.  SP: ng is even and the
+// scales/biases come in pairs of groups (one pair per loop iteration, loaded an iteration ahead).
+template <int BITS, bool BF16, int NB, int JB, bool SP>
 __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16* __restrict__ sA,
                                               const uint16_t* __restrict__ arow, const BRows<JB>& R, int ng) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -216,8 +247,14 @@ __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16*
   const int last = ng - 1;
   uint32_t ar[16];
   BGroup<JB> G0, G1;
-  load_group<BITS>(R, 0, G0);
-  load_group<BITS>(R, min(1, last), G1);
+  BScalePair<JB> S, Sn;
+  uint16_t sc[JB], bi[JB];
+  load_group<BITS, JB, !SP>(R, 0, G0);
+  load_group<BITS, JB, !SP>(R, min(1, last), G1);
+  if constexpr (SP) {
+    load_scale_pair(R, 0, S);
+    load_scale_pair(R, min(1, last >> 1), Sn);
+  }
   load16g(ag, ar);
   store16s(st, ar);
   load16g(ag + (size_t)min(1, last) * 64, ar);
@@ -225,18 +262,34 @@ __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16*
   // pairs of groups (slab 0, then slab 1), so the loop has one exit; an odd last group follows
   int g = 0;
   for (; g + 1 < ng; g += 2) {
-    gemm_group<BITS, BF16, NB>(acc, sA, lane, G0);
-    load_group<BITS>(R, min(g + 2, last), G0);
+    if constexpr (SP) {
+      pair_half(S, 0, sc, bi);
+      gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, sc, bi);
+    } else {
+      gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, G0.s, G0.b);
+    }
+    load_group<BITS, JB, !SP>(R, min(g + 2, last), G0);
     store16s(st + SLAB, ar);
     load16g(ag + (size_t)min(g + 2, last) * 64, ar);
     lds_barrier();
-    gemm_group<BITS, BF16, NB>(acc, sA + SLAB, lane, G1);
-    load_group<BITS>(R, min(g + 3, last), G1);
+    if constexpr (SP) {
+      pair_half(S, 1, sc, bi);
+      gemm_group<BITS, BF16, NB>(acc, sA + SLAB, lane, G1, sc, bi);
+    } else {
+      gemm_group<BITS, BF16, NB>(acc, sA + SLAB, lane, G1, G1.s, G1.b);
+    }
+    load_group<BITS, JB, !SP>(R, min(g + 3, last), G1);
+    if constexpr (SP) {
+      S = Sn;
+      load_scale_pair(R, min((g >> 1) + 2, last >> 1), Sn);
+    }
     store16s(st, ar);
     load16g(ag + (size_t)min(g + 3, last) * 64, ar);
     lds_barrier();
   }
-  if (g < ng) gemm_group<BITS, BF16, NB>(acc, sA, lane, G0);
+  if constexpr (!SP) {
+    if (g < ng) gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, G0.s, G0.b);
+  }
 }
 
 template <int JB>
@@ -258,7 +311,7 @@ constexpr int DN_COLS = 4 * 64;  // output columns per down workgroup
 // the 32 columns c0 = 128ct + 32w + n.  Each lane holds matching gate and up values and writes
 // act = silu(gate) * up (fp16, pair order within each 32-column chunk, the down projection's k
 // order) for the sorted position of each row.
-template <int BITS, bool BF16, int ACT, int NB>
+template <int BITS, bool BF16, int ACT, int NB, bool SP>
 __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* __restrict__ x, int K,
                                             const int32_t* __restrict__ perm, int e, int row0, int nrows, int ct,
                                             _Float16* sA, uint16_t* __restrict__ act) {
@@ -280,7 +333,7 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
   R.vs[0] = R.vs[1] = row * ng * 2u;
   float16_t acc[4][2];
   zero_acc(acc);
-  gemm_mainloop<BITS, BF16, NB>(acc, sA, x + (size_t)tok * H, R, (int)ng);
+  gemm_mainloop<BITS, BF16, NB, 2, SP>(acc, sA, x + (size_t)tok * H, R, (int)ng);
   if (c0 >= I) return;
   const int h = lane >> 5;
   uint16_t* const ap = act + (size_t)row0 * I + c0 + pairpos_p<BITS>(lane & 31);
@@ -294,7 +347,7 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
   }
 }
 
-template <int BITS, bool BF16, int ACT>
+template <int BITS, bool BF16, int ACT, bool SP>
 __global__ __launch_bounds__(256, 2) void gemm_gateup_kernel(const LayerArgs L, const uint16_t* __restrict__ x,
                                                              int K, const int32_t* __restrict__ perm,
                                                              const int32_t* __restrict__ scalars,
@@ -307,10 +360,10 @@ __global__ __launch_bounds__(256, 2) void gemm_gateup_kernel(const LayerArgs L, 
   if (!xcd_mtile(blockIdx.x, (L.I + GU_COLS - 1) / GU_COLS, uniform(scalars[1]), mt, ct)) return;
   const int e = uniform(mt_expert[mt]), row0 = uniform(mt_row0[mt]), nrows = uniform(mt_rows[mt]);
   switch ((nrows + 31) >> 5) {
-    case 1: gateup_tile<BITS, BF16, ACT, 1>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-    case 2: gateup_tile<BITS, BF16, ACT, 2>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-    case 3: gateup_tile<BITS, BF16, ACT, 3>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-    default: gateup_tile<BITS, BF16, ACT, 4>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    case 1: gateup_tile<BITS, BF16, ACT, 1, SP>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    case 2: gateup_tile<BITS, BF16, ACT, 2, SP>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    case 3: gateup_tile<BITS, BF16, ACT, 3, SP>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    default: gateup_tile<BITS, BF16, ACT, 4, SP>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
   }
 }
 
@@ -318,7 +371,7 @@ __global__ __launch_bounds__(256, 2) void gemm_gateup_kernel(const LayerArgs L, 
 // c0 + 32j + n with c0 = 256ct + 64w (j = 0, 1).  Row r of the tile (sorted position row0 + r)
 // is written to its assignment perm[row0 + r]: fp16 unweighted (the switch_mlp contract) or fp32
 // scaled by the assignment's routing weight (the fused layer, summed by combine_kernel).
-template <int BITS, bool BF16, bool OUT16, int NB>
+template <int BITS, bool BF16, bool OUT16, int NB, bool SP>
 __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, int nrows, int ct, _Float16* sA,
                                           const int32_t* s_asg, const float* s_wa,
                                           const uint16_t* __restrict__ act, float* __restrict__ y32,
@@ -343,7 +396,7 @@ __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, i
   }
   float16_t acc[4][2];
   zero_acc(acc);
-  gemm_mainloop<BITS, BF16, NB>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, R, (int)ng);
+  gemm_mainloop<BITS, BF16, NB, 2, SP>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, R, (int)ng);
   const int h = lane >> 5;
 #pragma unroll
   for (int mb = 0; mb < NB; ++mb) {
@@ -369,7 +422,7 @@ __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, i
   }
 }
 
-template <int BITS, bool BF16, bool OUT16>
+template <int BITS, bool BF16, bool OUT16, bool SP>
 __global__ __launch_bounds__(256, 2) void gemm_down_kernel(const LayerArgs L, const int32_t* __restrict__ perm,
                                                            const int32_t* __restrict__ scalars,
                                                            const int32_t* __restrict__ mt_expert,
@@ -391,10 +444,10 @@ __global__ __launch_bounds__(256, 2) void gemm_down_kernel(const LayerArgs L, co
     s_wa[tid] = wscale && tid < nrows ? wscale[a] : 1.0f;
   }
   switch ((nrows + 31) >> 5) {
-    case 1: down_tile<BITS, BF16, OUT16, 1>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-    case 2: down_tile<BITS, BF16, OUT16, 2>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-    case 3: down_tile<BITS, BF16, OUT16, 3>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-    default: down_tile<BITS, BF16, OUT16, 4>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    case 1: down_tile<BITS, BF16, OUT16, 1, SP>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    case 2: down_tile<BITS, BF16, OUT16, 2, SP>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    case 3: down_tile<BITS, BF16, OUT16, 3, SP>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    default: down_tile<BITS, BF16, OUT16, 4, SP>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
   }
 }
 
@@ -448,19 +501,28 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
   const LayerArgs& L = c.args;
   (void)T;
   const int per_xcd = (max_mtiles + 7) / 8;  // m-tiles of one XCD's share at most (see xcd_mtile)
-  KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT>), dim3(8 * per_xcd * ((L.I + GU_COLS - 1) / GU_COLS)),
-              dim3(256), 0, s, L, x, c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act);
+  const dim3 grid_gu(8 * per_xcd * ((L.I + GU_COLS - 1) / GU_COLS));
+  // scales in pairs of groups when the rows hold an even number of groups
+  if ((L.H / GROUP) % 2 == 0)
+    KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, true>), grid_gu, dim3(256), 0, s, L, x,
+                c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act);
+  else
+    KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, false>), grid_gu, dim3(256), 0, s, L, x,
+                c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  const dim3 grid_down(8 * per_xcd * ((L.H + DN_COLS - 1) / DN_COLS));
+  const dim3 grid_dn(8 * per_xcd * ((L.H + DN_COLS - 1) / DN_COLS));
+  const bool sp = (L.I / GROUP) % 2 == 0;
+#define KMOE_DOWN(OUT16, SPV)                                                                                  \
+  KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, OUT16, SPV>), grid_dn, dim3(256), 0, s, L, w.perm, \
+              w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale,                    \
+              OUT16 ? (float*)nullptr : w.y32, OUT16 ? y16 : (uint16_t*)nullptr)
   if (y16) {
-    KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, true>), grid_down, dim3(256), 0, s, L, w.perm,
-                w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale, (float*)nullptr, y16);
+    if (sp) KMOE_DOWN(true, true); else KMOE_DOWN(true, false);
   } else {
-    KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, false>), grid_down, dim3(256), 0, s, L, w.perm,
-                w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale, w.y32,
-                (uint16_t*)nullptr);
+    if (sp) KMOE_DOWN(false, true); else KMOE_DOWN(false, false);
   }
+#undef KMOE_DOWN
   return hipGetLastError();
 }
 
