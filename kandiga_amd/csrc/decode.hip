@@ -16,14 +16,17 @@
 //     applies s*2^24*dot + b*sum(x) per chunk, reduces all 2*RW values across the wave in one
 //     pass and writes act = silu(gate) * up as two fp16 planes (hi, lo: hi + lo carries ~22
 //     bits) in pair order.
-//   dec_stage2_kernel: grid = blocks of S2_ROWS output rows.  Lanes are (assignment, 32-wide
-//     chunk of the intermediate dimension) over RPW rows of the down projection; each lane
+//   dec_stage2_kernel: grid = blocks of S2_ROWS output rows x groups of tokens.  Lanes are
+//     (assignment, 32-wide chunk of the intermediate dimension) over RPW rows of the down
+//     projection; each lane
 //     dots its act chunk (hi and lo planes) with the rows' codes, the per-assignment row totals
 //     go to LDS and are combined in k order with the routing weights (moe_block.metal:515-539),
 //     so the fused combine is deterministic.  The per-assignment variant writes y[t,k,:]
 //     instead (the switch_mlp contract, engine.py:670-739).
 #include "kmoe_device.h"
 #include "kmoe_internal.h"
+
+#include <type_traits>
 
 namespace kmoe {
 
@@ -323,9 +326,25 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int 
                                                          const float* __restrict__ wts,
                                                          const uint16_t* __restrict__ act, size_t act_plane,
                                                          void* __restrict__ out, int out32,
-                                                         const float* __restrict__ shared_out, int lpa_log2) {
+                                                         const float* __restrict__ shared_out, int lpa_log2, int TG) {
   __shared__ float red[DEC_STAGE2_ASSIGN * S2_ROWS];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // Token group blockIdx.y: tokens [t0, t0 + TG) are handled as a call of their own, so a
+  // workgroup loads the act rows of only TG*K assignments for its output rows.
+  {
+    const int t0 = blockIdx.y * TG;
+    T = min(TG, T - t0);
+    idx += t0 * K;
+    if (COMBINE) wts += t0 * K;
+    act += (size_t)t0 * K * L.I;
+    if (COMBINE) {
+      out = out32 ? static_cast<void*>(static_cast<float*>(out) + (size_t)t0 * L.H)
+                  : static_cast<void*>(static_cast<uint16_t*>(out) + (size_t)t0 * L.H);
+      if (shared_out) shared_out += (size_t)t0 * L.H;
+    } else {
+      out = static_cast<uint16_t*>(out) + (size_t)t0 * K * L.H;
+    }
+  }
   const int H = L.H, I = L.I, E = L.E, nchI = I / CHUNK, TK = T * K;
   KMOE_MARK(1, 0);
   // routing of assignment a = t*K + k sits in lane a % 64 of slot a / 64 (T*K <= 128)
@@ -545,21 +564,39 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
                    : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false>, grid1, s, A);
   if (err != hipSuccess) return err;
   const int l2 = lpa_log2_for(L.I);
-  // output rows per workgroup and per unit: the single-token layer has few units, so a unit's
-  // rows are split between waves; more tokens give enough units for 4-row units on a doubled grid
-  constexpr int S2_ROWS = NT == 1 ? 8 : 4;
-  constexpr int RPW = 4;
-  constexpr int UF = 2;
+  // Output rows per workgroup (S2_ROWS) and per lane (RPW), and tokens per workgroup (TG).  Every
+  // workgroup re-reads the act rows of its tokens' assignments, so taller row blocks cut that
+  // traffic; the tokens are then split into groups over a second grid dimension, sized for about
+  // two workgroups per CU (measured best at hidden 2048 and 4096, 4 and 8 tokens) with at least
+  // 8 assignments per workgroup.  Below 32 assignments short row blocks over all tokens are
+  // faster.
   const int32_t* idx = d.idx_in ? d.idx_in : d.idx_out;
-  const dim3 grid2(L.H / S2_ROWS);
-  if (d.combine) {
-    KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, S2_ROWS, RPW, UF, true>), grid2, dim3(256), 0, s, L, T,
-                K, idx, d.wts, (const uint16_t*)w.act, A.act_plane, d.out, d.out32,
-                L.sh_gate ? (const float*)w.shared_out : (const float*)nullptr, l2);
+  const float* sho = L.sh_gate ? (const float*)w.shared_out : (const float*)nullptr;
+  auto stage2 = [&](auto srows, auto rpw, int TG) {
+    constexpr int SR = decltype(srows)::value, RP = decltype(rpw)::value, UF = 2;
+    const dim3 grid2(L.H / SR, (T + TG - 1) / TG);
+    if (d.combine) {
+      KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, true>), grid2, dim3(256), 0, s, L,
+                  T, K, idx, d.wts, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, l2, TG);
+    } else {
+      KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, false>), grid2, dim3(256), 0, s,
+                  L, T, K, idx, (const float*)nullptr, (const uint16_t*)w.act, A.act_plane, d.out, 0,
+                  (const float*)nullptr, l2, TG);
+    }
+  };
+  using I4 = std::integral_constant<int, 4>;
+  using I8 = std::integral_constant<int, 8>;
+  using I16 = std::integral_constant<int, 16>;
+  if constexpr (NT == 1) {
+    stage2(I8{}, I4{}, T);
+  } else if constexpr (NT == 2) {
+    stage2(I4{}, I4{}, T);
   } else {
-    KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, S2_ROWS, RPW, UF, false>), grid2, dim3(256), 0, s, L, T,
-                K, idx, (const float*)nullptr, (const uint16_t*)w.act, A.act_plane, d.out, 0,
-                (const float*)nullptr, l2);
+    if (T * K >= 32) {
+      const int tg = T * (L.H / 16) / (2 * cu_count());
+      stage2(I16{}, I8{}, min(T, max(tg, (8 + K - 1) / K)));
+    } else
+      stage2(I4{}, I4{}, T);
   }
   return hipGetLastError();
 }
