@@ -55,6 +55,8 @@ def parse():
                    help="decode cases tokens:top_k, comma separated ('' for none)")
     p.add_argument("--prefill", default="512,2048,4096", help="prefill token counts ('' for none)")
     p.add_argument("--modes", default="graph,eager", help="decode launch modes")
+    p.add_argument("--no-prefill-copy", dest="prefill_copy", action="store_false",
+                   help="skip the prefill runs that read the weights from a prefill copy")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-shared-layer", dest="shared_layer", action="store_false",
@@ -219,6 +221,11 @@ def main():
     prefill = {}
     for T in [int(v) for v in args.prefill.split(",") if v]:
         prefill[f"prefill_T{T}"] = prefill_case(experts[8][0], shape, T)
+    if args.prefill_copy and args.prefill:
+        ex_pk = experts[8][0].with_prefill_copy()
+        for T in [int(v) for v in args.prefill.split(",") if v]:
+            prefill[f"prefill_copy_T{T}"] = prefill_case(ex_pk, shape, T, " (prefill copy)")
+        del ex_pk
 
     # the hidden-2560 layer with a dense fp16 shared expert (decode over 4 rotated layers)
     if args.shared_layer:

@@ -74,6 +74,12 @@ typedef struct {
   const void* shared_down;
   int32_t shared_intermediate;
   int32_t reserved;
+  /* Optional prefill copy of the routed experts made by kmoe_prefill_pack from this same
+     description (device, 256-byte aligned, kmoe_prefill_pack_size bytes), or NULL.  When set,
+     the grouped GEMMs of calls with more than 8 tokens read the weights from it; decode and the
+     dequantization check keep reading the MLX-layout tensors above. */
+  const void* prefill_pack;
+  int64_t prefill_pack_bytes;
 } kmoe_layer_desc;
 
 typedef struct kmoe_layer kmoe_layer;
@@ -149,6 +155,20 @@ int kmoe_combine(const void* y, const float* weights, int32_t tokens, int32_t to
 int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                  int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
                  void* stream);
+
+/*
+ * Prefill weight copy.  No counterpart in the reference, whose routed experts exist only in
+ * the MLX layout; for callers that run prefill and can hold a second copy of the experts (about
+ * the size of the codes plus scales).  kmoe_prefill_pack rewrites every expert of `desc` into a
+ * layout in which one wavefront load of the grouped GEMMs reads whole cache lines:
+ *   codes  [expert][32-row block][group][lane n + 32h][chunk h of row n]   (12 or 16 bytes)
+ *   scales/biases [expert][32-row block][group pair][row n][s0 s1 b0 b1]   (fp16/bf16 bits)
+ * for gate, up and down in turn (each region 256-byte aligned).  Results do not depend on
+ * whether a layer has the copy.  `pack` is device memory of kmoe_prefill_pack_size bytes;
+ * the call is asynchronous on `stream` and reads the tensors `desc` points to.
+ */
+int kmoe_prefill_pack_size(const kmoe_layer_desc* desc, size_t* bytes);
+int kmoe_prefill_pack(const kmoe_layer_desc* desc, void* pack, size_t bytes, void* stream);
 
 /*
  * Dequantization check: codes (uint8 [nrows][in]) and fp16 weights round(q*s + b)

@@ -19,6 +19,7 @@ EXPORTS = (
     "kmoe_layer_create", "kmoe_layer_destroy", "kmoe_workspace_size",
     "kmoe_route", "kmoe_permute_workspace_size", "kmoe_permute",
     "kmoe_expert_mlp", "kmoe_combine", "kmoe_forward",
+    "kmoe_prefill_pack_size", "kmoe_prefill_pack",
     "kmoe_dequantize", "kmoe_device_status",
     "kmoe_profile_begin", "kmoe_profile_end",
 )
@@ -52,7 +53,8 @@ class LayerDesc(ctypes.Structure):
                 ("scale_dtype", ctypes.c_int32), ("activation", ctypes.c_int32),
                 ("gate", QProjDesc), ("up", QProjDesc), ("down", QProjDesc),
                 ("shared_gate", ctypes.c_void_p), ("shared_up", ctypes.c_void_p), ("shared_down", ctypes.c_void_p),
-                ("shared_intermediate", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("shared_intermediate", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("prefill_pack", ctypes.c_void_p), ("prefill_pack_bytes", ctypes.c_int64)]
 
 
 class KernelTime(ctypes.Structure):
@@ -79,6 +81,8 @@ def _declare(L):
         "kmoe_expert_mlp": ([_vp, _vp, _vp, _i32, _vp, _vp, _sz, _vp], ctypes.c_int),
         "kmoe_combine": ([_vp, _vp, _i32, _i32, _i32, _vp, _vp], ctypes.c_int),
         "kmoe_forward": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
+        "kmoe_prefill_pack_size": ([P(LayerDesc), P(_sz)], ctypes.c_int),
+        "kmoe_prefill_pack": ([P(LayerDesc), _vp, _sz, _vp], ctypes.c_int),
         "kmoe_dequantize": ([_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp], ctypes.c_int),
         "kmoe_device_status": ([_vp, _sz, P(_i32), _vp], ctypes.c_int),
         "kmoe_profile_begin": ([_i32], ctypes.c_int),

@@ -153,9 +153,8 @@ const char* kmoe_strerror(int status) {
 
 const char* kmoe_last_error(void) { return g_last_error.c_str(); }
 
-int kmoe_layer_create(const kmoe_layer_desc* d, kmoe_layer** out) {
-  if (!d || !out) return fail(KMOE_ERR_INVALID_ARG, "null descriptor or output pointer");
-  *out = nullptr;
+// Validates a layer description and fills `cfg` from it (the prefill copy fields aside).
+static int config_from_desc(const kmoe_layer_desc* d, LayerConfig* cfg) {
   if (d->bits != 3 && d->bits != 4) return fail(KMOE_ERR_UNSUPPORTED, "bits must be 3 or 4 (got %d)", d->bits);
   if (d->group_size != 64) return fail(KMOE_ERR_UNSUPPORTED, "group_size must be 64 (got %d)", d->group_size);
   if (d->hidden <= 0 || d->hidden % 64 || d->hidden > 65536)
@@ -186,9 +185,8 @@ int kmoe_layer_create(const kmoe_layer_desc* d, kmoe_layer** out) {
     if (!aligned(d->shared_gate, 16) || !aligned(d->shared_up, 16) || !aligned(d->shared_down, 16))
       return fail(KMOE_ERR_ALIGNMENT, "shared expert weights must be 16-byte aligned");
   }
-  kmoe_layer* L = new (std::nothrow) kmoe_layer;
-  if (!L) return fail(KMOE_ERR_NO_MEMORY, "out of host memory");
-  LayerArgs& a = L->cfg.args;
+  LayerArgs& a = cfg->args;
+  a = LayerArgs{};
   auto qp = [](const kmoe_qproj& q) {
     return QProj{static_cast<const uint8_t*>(q.weight), static_cast<const uint16_t*>(q.scales),
                  static_cast<const uint16_t*>(q.biases), q.weight_expert_stride, q.scale_expert_stride / 2};
@@ -203,12 +201,56 @@ int kmoe_layer_create(const kmoe_layer_desc* d, kmoe_layer** out) {
   a.I = d->intermediate;
   a.E = d->num_experts;
   a.Is = any_shared ? d->shared_intermediate : 0;
-  L->cfg.top_k = d->top_k;
-  L->cfg.bits = d->bits;
-  L->cfg.bf16_scales = d->scale_dtype == KMOE_SCALE_BF16;
-  L->cfg.act = d->activation;
+  cfg->top_k = d->top_k;
+  cfg->bits = d->bits;
+  cfg->bf16_scales = d->scale_dtype == KMOE_SCALE_BF16;
+  cfg->act = d->activation;
+  return KMOE_OK;
+}
+
+int kmoe_layer_create(const kmoe_layer_desc* d, kmoe_layer** out) {
+  if (!d || !out) return fail(KMOE_ERR_INVALID_ARG, "null descriptor or output pointer");
+  *out = nullptr;
+  LayerConfig cfg{};
+  int rc;
+  if ((rc = config_from_desc(d, &cfg))) return rc;
+  if (d->prefill_pack) {
+    const PackLayout pl = pack_layout(cfg.args.H, cfg.args.I, cfg.args.E, cfg.bits);
+    if (!aligned(d->prefill_pack, 256)) return fail(KMOE_ERR_ALIGNMENT, "prefill_pack must be 256-byte aligned");
+    if (d->prefill_pack_bytes < pl.total)
+      return fail(KMOE_ERR_INVALID_ARG, "prefill_pack_bytes %lld below the %lld bytes of the copy",
+                  (long long)d->prefill_pack_bytes, (long long)pl.total);
+    const uint8_t* base = static_cast<const uint8_t*>(d->prefill_pack);
+    for (int q = 0; q < 3; ++q)
+      cfg.args.pk[q] = PackProj{base + pl.codes[q], base + pl.sb[q], pl.codes_expert[q], pl.sb_expert[q]};
+  }
+  kmoe_layer* L = new (std::nothrow) kmoe_layer;
+  if (!L) return fail(KMOE_ERR_NO_MEMORY, "out of host memory");
+  L->cfg = cfg;
   *out = L;
   return ok();
+}
+
+int kmoe_prefill_pack_size(const kmoe_layer_desc* d, size_t* bytes) {
+  if (!d || !bytes) return fail(KMOE_ERR_INVALID_ARG, "null descriptor or output pointer");
+  LayerConfig cfg{};
+  int rc;
+  if ((rc = config_from_desc(d, &cfg))) return rc;
+  *bytes = (size_t)pack_layout(cfg.args.H, cfg.args.I, cfg.args.E, cfg.bits).total;
+  return ok();
+}
+
+int kmoe_prefill_pack(const kmoe_layer_desc* d, void* pack, size_t bytes, void* stream) {
+  if (!d || !pack) return fail(KMOE_ERR_INVALID_ARG, "null descriptor or pack pointer");
+  LayerConfig cfg{};
+  int rc;
+  if ((rc = config_from_desc(d, &cfg))) return rc;
+  const PackLayout pl = pack_layout(cfg.args.H, cfg.args.I, cfg.args.E, cfg.bits);
+  if (!aligned(pack, 256)) return fail(KMOE_ERR_ALIGNMENT, "pack must be 256-byte aligned");
+  if (bytes < (size_t)pl.total)
+    return fail(KMOE_ERR_INVALID_ARG, "pack holds %zu bytes, the copy needs %lld", bytes, (long long)pl.total);
+  const hipError_t e = launch_prefill_pack(cfg, static_cast<uint8_t*>(pack), static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "prefill pack launch");
 }
 
 int kmoe_layer_destroy(kmoe_layer* layer) {

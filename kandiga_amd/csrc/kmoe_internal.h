@@ -17,8 +17,26 @@ struct QProj {
   int64_t s_stride;  // uint16 elements
 };
 
+// One projection of the prefill weight copy (kmoe_prefill_pack): codes of expert e at
+// codes + e*codes_expert, laid out [32-row block][group][lane][chunk]; scales and biases at
+// sb + e*sb_expert, [32-row block][group pair][row][s0 s1 b0 b1].  Null codes: no copy.
+struct PackProj {
+  const uint8_t* codes;
+  const uint8_t* sb;
+  int64_t codes_expert;  // bytes per expert
+  int64_t sb_expert;     // bytes per expert
+};
+
+// Byte offsets of the six regions of a prefill copy (gate/up/down codes, then gate/up/down
+// scale-bias pairs, each 256-byte aligned) and its total size.
+struct PackLayout {
+  int64_t codes[3], sb[3], codes_expert[3], sb_expert[3], total;
+};
+PackLayout pack_layout(int H, int I, int E, int bits);
+
 struct LayerArgs {
   QProj gate, up, down;
+  PackProj pk[3];  // gate, up, down of the prefill copy (codes null when absent)
   const uint16_t* sh_gate;  // dense fp16 shared expert [Is][H] (or null)
   const uint16_t* sh_up;    // [Is][H]
   const uint16_t* sh_down;  // [H][Is]
@@ -110,6 +128,8 @@ hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Wor
 hipError_t launch_combine(const float* y32, const uint16_t* y16, const float* wts, int T, int K, int H,
                           const float* shared, void* out, int out32, hipStream_t s);
 hipError_t launch_shared(const LayerConfig& c, const uint16_t* x, int T, const Work& w, hipStream_t s);
+// Writes the prefill copy of c's experts into `pack` (laid out by pack_layout).
+hipError_t launch_prefill_pack(const LayerConfig& c, uint8_t* pack, hipStream_t s);
 hipError_t launch_dequantize(const LayerConfig& c, int proj, int expert, int row0, int nrows, uint8_t* codes,
                              uint16_t* wf16, hipStream_t s);
 

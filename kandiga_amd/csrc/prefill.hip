@@ -156,11 +156,13 @@ template <int JB>
 struct BRows {
   __amdgpu_buffer_rsrc_t rw[JB], rs[JB], rb[JB];
   uint32_t vw[JB], vs[JB];
+  uint32_t gstride;  // code bytes from one group to the next at the same lane offset
+  uint32_t pstride;  // scale bytes from one group pair to the next
 };
 
 template <int BITS, int JB, bool SCALES>
 __device__ __forceinline__ void load_group(const BRows<JB>& R, int g, BGroup<JB>& G) {
-  const uint32_t sw = (uint32_t)uniform(g * 2 * Bits<BITS>::chunk_bytes), ss = (uint32_t)uniform(g * 2);
+  const uint32_t sw = (uint32_t)uniform(g * (int)R.gstride), ss = (uint32_t)uniform(g * 2);
 #pragma unroll
   for (int j = 0; j < JB; ++j) {
     buf_chunk_cached<BITS>(R.rw[j], R.vw[j], sw, G.d[j]);
@@ -171,13 +173,20 @@ __device__ __forceinline__ void load_group(const BRows<JB>& R, int g, BGroup<JB>
   }
 }
 
-template <int JB>
+// PK: the prefill copy holds s0 s1 b0 b1 of a row side by side (one 8-byte load).
+template <int JB, bool PK>
 __device__ __forceinline__ void load_scale_pair(const BRows<JB>& R, int p, BScalePair<JB>& S) {
-  const uint32_t ss = (uint32_t)uniform(p * 4);
+  const uint32_t ss = (uint32_t)uniform(p * (int)R.pstride);
 #pragma unroll
   for (int j = 0; j < JB; ++j) {
-    S.s[j] = __builtin_amdgcn_raw_buffer_load_b32(R.rs[j], R.vs[j], ss, 0);
-    S.b[j] = __builtin_amdgcn_raw_buffer_load_b32(R.rb[j], R.vs[j], ss, 0);
+    if constexpr (PK) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(R.rs[j], R.vs[j], ss, 0);
+      S.s[j] = v[0];
+      S.b[j] = v[1];
+    } else {
+      S.s[j] = __builtin_amdgcn_raw_buffer_load_b32(R.rs[j], R.vs[j], ss, 0);
+      S.b[j] = __builtin_amdgcn_raw_buffer_load_b32(R.rb[j], R.vs[j], ss, 0);
+    }
   }
 }
 
@@ -236,11 +245,14 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 // The k loop over ng groups.  Thread t stages half (t & 1) of slab row t >> 1 from arow (a row
 // of ng*64 halves).  Every load is unconditional (past the last group the index is clamped,
-// re-reading that group), so the wait counts before each use are exact.  SP: ng is even and the
-// scales/biases come in pairs of groups (one pair per loop iteration, loaded an iteration ahead).
-template <int BITS, bool BF16, int NB, int JB, bool SP>
+// re-reading that group), so the wait counts before each use are exact.  BL selects where the
+// weights come from: 0 the MLX tensors with per-group scales; 1 the MLX tensors with scales
+// and biases in pairs of groups (one pair per loop iteration, loaded an iteration ahead; ng
+// even); 2 the prefill copy (pairs padded to even, so ng may be odd).
+template <int BITS, bool BF16, int NB, int JB, int BL>
 __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16* __restrict__ sA,
                                               const uint16_t* __restrict__ arow, const BRows<JB>& R, int ng) {
+  constexpr bool SP = BL >= 1, PK = BL == 2;
   const int tid = threadIdx.x, lane = tid & 63;
   _Float16* const st = sA + (tid >> 1) * LDA + 32 * (tid & 1);
   const uint16_t* const ag = arow + 32 * (tid & 1);
@@ -252,8 +264,8 @@ __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16*
   load_group<BITS, JB, !SP>(R, 0, G0);
   load_group<BITS, JB, !SP>(R, min(1, last), G1);
   if constexpr (SP) {
-    load_scale_pair(R, 0, S);
-    load_scale_pair(R, min(1, last >> 1), Sn);
+    load_scale_pair<JB, PK>(R, 0, S);
+    load_scale_pair<JB, PK>(R, min(1, last >> 1), Sn);
   }
   load16g(ag, ar);
   store16s(st, ar);
@@ -281,14 +293,19 @@ __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16*
     load_group<BITS, JB, !SP>(R, min(g + 3, last), G1);
     if constexpr (SP) {
       S = Sn;
-      load_scale_pair(R, min((g >> 1) + 2, last >> 1), Sn);
+      load_scale_pair<JB, PK>(R, min((g >> 1) + 2, last >> 1), Sn);
     }
     store16s(st, ar);
     load16g(ag + (size_t)min(g + 3, last) * 64, ar);
     lds_barrier();
   }
-  if constexpr (!SP) {
-    if (g < ng) gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, G0.s, G0.b);
+  if (g < ng) {  // an odd last group (scale pairs: the low half of the last, padded pair)
+    if constexpr (SP) {
+      pair_half(S, 0, sc, bi);
+      gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, sc, bi);
+    } else {
+      gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, G0.s, G0.b);
+    }
   }
 }
 
@@ -311,7 +328,7 @@ constexpr int DN_COLS = 4 * 64;  // output columns per down workgroup
 // the 32 columns c0 = 128ct + 32w + n.  Each lane holds matching gate and up values and writes
 // act = silu(gate) * up (fp16, pair order within each 32-column chunk, the down projection's k
 // order) for the sorted position of each row.
-template <int BITS, bool BF16, int ACT, int NB, bool SP>
+template <int BITS, bool BF16, int ACT, int NB, int BL>
 __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* __restrict__ x, int K,
                                             const int32_t* __restrict__ perm, int e, int row0, int nrows, int ct,
                                             _Float16* sA, uint16_t* __restrict__ act) {
@@ -322,18 +339,35 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
   const int c0 = ct * GU_COLS + wave * 32;
   const uint32_t rbytes = (uint32_t)H * BITS / 8, ng = (uint32_t)H / GROUP;
   BRows<2> R;
-  const uint32_t row = (uint32_t)(c0 + (lane & 31));
-  R.rw[0] = make_rsrc(L.gate.w + (size_t)e * L.gate.w_stride, (uint32_t)I * rbytes);
-  R.rw[1] = make_rsrc(L.up.w + (size_t)e * L.up.w_stride, (uint32_t)I * rbytes);
-  R.rs[0] = make_rsrc(L.gate.s + (size_t)e * L.gate.s_stride, (uint32_t)I * ng * 2u);
-  R.rb[0] = make_rsrc(L.gate.b + (size_t)e * L.gate.s_stride, (uint32_t)I * ng * 2u);
-  R.rs[1] = make_rsrc(L.up.s + (size_t)e * L.up.s_stride, (uint32_t)I * ng * 2u);
-  R.rb[1] = make_rsrc(L.up.b + (size_t)e * L.up.s_stride, (uint32_t)I * ng * 2u);
-  R.vw[0] = R.vw[1] = row * rbytes + (uint32_t)(lane >> 5) * Bits<BITS>::chunk_bytes;
-  R.vs[0] = R.vs[1] = row * ng * 2u;
+  if constexpr (BL == 2) {
+    const PackProj &pg = L.pk[0], &pu = L.pk[1];
+    const uint32_t rbk = (uint32_t)(c0 >> 5), npair = (ng + 1) / 2;
+    R.rw[0] = make_rsrc(pg.codes + (size_t)e * pg.codes_expert, (uint32_t)pg.codes_expert);
+    R.rw[1] = make_rsrc(pu.codes + (size_t)e * pu.codes_expert, (uint32_t)pu.codes_expert);
+    R.rs[0] = make_rsrc(pg.sb + (size_t)e * pg.sb_expert, (uint32_t)pg.sb_expert);
+    R.rs[1] = make_rsrc(pu.sb + (size_t)e * pu.sb_expert, (uint32_t)pu.sb_expert);
+    R.rb[0] = R.rs[0];
+    R.rb[1] = R.rs[1];
+    R.vw[0] = R.vw[1] = (rbk * ng * 64u + (uint32_t)lane) * Bits<BITS>::chunk_bytes;
+    R.vs[0] = R.vs[1] = (rbk * npair * 32u + (uint32_t)(lane & 31)) * 8u;
+    R.gstride = 64u * Bits<BITS>::chunk_bytes;
+    R.pstride = 256u;
+  } else {
+    const uint32_t row = (uint32_t)(c0 + (lane & 31));
+    R.rw[0] = make_rsrc(L.gate.w + (size_t)e * L.gate.w_stride, (uint32_t)I * rbytes);
+    R.rw[1] = make_rsrc(L.up.w + (size_t)e * L.up.w_stride, (uint32_t)I * rbytes);
+    R.rs[0] = make_rsrc(L.gate.s + (size_t)e * L.gate.s_stride, (uint32_t)I * ng * 2u);
+    R.rb[0] = make_rsrc(L.gate.b + (size_t)e * L.gate.s_stride, (uint32_t)I * ng * 2u);
+    R.rs[1] = make_rsrc(L.up.s + (size_t)e * L.up.s_stride, (uint32_t)I * ng * 2u);
+    R.rb[1] = make_rsrc(L.up.b + (size_t)e * L.up.s_stride, (uint32_t)I * ng * 2u);
+    R.vw[0] = R.vw[1] = row * rbytes + (uint32_t)(lane >> 5) * Bits<BITS>::chunk_bytes;
+    R.vs[0] = R.vs[1] = row * ng * 2u;
+    R.gstride = 2u * Bits<BITS>::chunk_bytes;
+    R.pstride = 4u;
+  }
   float16_t acc[4][2];
   zero_acc(acc);
-  gemm_mainloop<BITS, BF16, NB, 2, SP>(acc, sA, x + (size_t)tok * H, R, (int)ng);
+  gemm_mainloop<BITS, BF16, NB, 2, BL>(acc, sA, x + (size_t)tok * H, R, (int)ng);
   if (c0 >= I) return;
   const int h = lane >> 5;
   uint16_t* const ap = act + (size_t)row0 * I + c0 + pairpos_p<BITS>(lane & 31);
@@ -347,7 +381,7 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
   }
 }
 
-template <int BITS, bool BF16, int ACT, bool SP>
+template <int BITS, bool BF16, int ACT, int BL>
 __global__ __launch_bounds__(256, 2) void gemm_gateup_kernel(const LayerArgs L, const uint16_t* __restrict__ x,
                                                              int K, const int32_t* __restrict__ perm,
                                                              const int32_t* __restrict__ scalars,
@@ -360,10 +394,10 @@ __global__ __launch_bounds__(256, 2) void gemm_gateup_kernel(const LayerArgs L, 
   if (!xcd_mtile(blockIdx.x, (L.I + GU_COLS - 1) / GU_COLS, uniform(scalars[1]), mt, ct)) return;
   const int e = uniform(mt_expert[mt]), row0 = uniform(mt_row0[mt]), nrows = uniform(mt_rows[mt]);
   switch ((nrows + 31) >> 5) {
-    case 1: gateup_tile<BITS, BF16, ACT, 1, SP>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-    case 2: gateup_tile<BITS, BF16, ACT, 2, SP>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-    case 3: gateup_tile<BITS, BF16, ACT, 3, SP>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-    default: gateup_tile<BITS, BF16, ACT, 4, SP>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    case 1: gateup_tile<BITS, BF16, ACT, 1, BL>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    case 2: gateup_tile<BITS, BF16, ACT, 2, BL>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    case 3: gateup_tile<BITS, BF16, ACT, 3, BL>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    default: gateup_tile<BITS, BF16, ACT, 4, BL>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
   }
 }
 
@@ -371,7 +405,7 @@ __global__ __launch_bounds__(256, 2) void gemm_gateup_kernel(const LayerArgs L, 
 // c0 + 32j + n with c0 = 256ct + 64w (j = 0, 1).  Row r of the tile (sorted position row0 + r)
 // is written to its assignment perm[row0 + r]: fp16 unweighted (the switch_mlp contract) or fp32
 // scaled by the assignment's routing weight (the fused layer, summed by combine_kernel).
-template <int BITS, bool BF16, bool OUT16, int NB, bool SP>
+template <int BITS, bool BF16, bool OUT16, int NB, int BL>
 __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, int nrows, int ct, _Float16* sA,
                                           const int32_t* s_asg, const float* s_wa,
                                           const uint16_t* __restrict__ act, float* __restrict__ y32,
@@ -382,21 +416,41 @@ __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, i
   const int c0 = ct * DN_COLS + wave * 64;
   const uint32_t rbytes = (uint32_t)I * BITS / 8, ng = (uint32_t)I / GROUP;
   BRows<2> R;
-  const auto dw = make_rsrc(L.down.w + (size_t)e * L.down.w_stride, (uint32_t)H * rbytes);
-  const auto ds = make_rsrc(L.down.s + (size_t)e * L.down.s_stride, (uint32_t)H * ng * 2u);
-  const auto db = make_rsrc(L.down.b + (size_t)e * L.down.s_stride, (uint32_t)H * ng * 2u);
+  if constexpr (BL == 2) {
+    const PackProj& pd = L.pk[2];
+    const uint32_t npair = (ng + 1) / 2;
+    const auto dw = make_rsrc(pd.codes + (size_t)e * pd.codes_expert, (uint32_t)pd.codes_expert);
+    const auto dsb = make_rsrc(pd.sb + (size_t)e * pd.sb_expert, (uint32_t)pd.sb_expert);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const uint32_t row = (uint32_t)(c0 + 32 * j + (lane & 31));
-    R.rw[j] = dw;
-    R.rs[j] = ds;
-    R.rb[j] = db;
-    R.vw[j] = row * rbytes + (uint32_t)(lane >> 5) * Bits<BITS>::chunk_bytes;
-    R.vs[j] = row * ng * 2u;
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t rbk = (uint32_t)(c0 >> 5) + (uint32_t)j;
+      R.rw[j] = dw;
+      R.rs[j] = dsb;
+      R.rb[j] = dsb;
+      R.vw[j] = (rbk * ng * 64u + (uint32_t)lane) * Bits<BITS>::chunk_bytes;
+      R.vs[j] = (rbk * npair * 32u + (uint32_t)(lane & 31)) * 8u;
+    }
+    R.gstride = 64u * Bits<BITS>::chunk_bytes;
+    R.pstride = 256u;
+  } else {
+    const auto dw = make_rsrc(L.down.w + (size_t)e * L.down.w_stride, (uint32_t)H * rbytes);
+    const auto ds = make_rsrc(L.down.s + (size_t)e * L.down.s_stride, (uint32_t)H * ng * 2u);
+    const auto db = make_rsrc(L.down.b + (size_t)e * L.down.s_stride, (uint32_t)H * ng * 2u);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t row = (uint32_t)(c0 + 32 * j + (lane & 31));
+      R.rw[j] = dw;
+      R.rs[j] = ds;
+      R.rb[j] = db;
+      R.vw[j] = row * rbytes + (uint32_t)(lane >> 5) * Bits<BITS>::chunk_bytes;
+      R.vs[j] = row * ng * 2u;
+    }
+    R.gstride = 2u * Bits<BITS>::chunk_bytes;
+    R.pstride = 4u;
   }
   float16_t acc[4][2];
   zero_acc(acc);
-  gemm_mainloop<BITS, BF16, NB, 2, SP>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, R, (int)ng);
+  gemm_mainloop<BITS, BF16, NB, 2, BL>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, R, (int)ng);
   const int h = lane >> 5;
 #pragma unroll
   for (int mb = 0; mb < NB; ++mb) {
@@ -422,7 +476,7 @@ __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, i
   }
 }
 
-template <int BITS, bool BF16, bool OUT16, bool SP>
+template <int BITS, bool BF16, bool OUT16, int BL>
 __global__ __launch_bounds__(256, 2) void gemm_down_kernel(const LayerArgs L, const int32_t* __restrict__ perm,
                                                            const int32_t* __restrict__ scalars,
                                                            const int32_t* __restrict__ mt_expert,
@@ -444,10 +498,10 @@ __global__ __launch_bounds__(256, 2) void gemm_down_kernel(const LayerArgs L, co
     s_wa[tid] = wscale && tid < nrows ? wscale[a] : 1.0f;
   }
   switch ((nrows + 31) >> 5) {
-    case 1: down_tile<BITS, BF16, OUT16, 1, SP>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-    case 2: down_tile<BITS, BF16, OUT16, 2, SP>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-    case 3: down_tile<BITS, BF16, OUT16, 3, SP>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-    default: down_tile<BITS, BF16, OUT16, 4, SP>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    case 1: down_tile<BITS, BF16, OUT16, 1, BL>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    case 2: down_tile<BITS, BF16, OUT16, 2, BL>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    case 3: down_tile<BITS, BF16, OUT16, 3, BL>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    default: down_tile<BITS, BF16, OUT16, 4, BL>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
   }
 }
 
@@ -502,25 +556,27 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
   (void)T;
   const int per_xcd = (max_mtiles + 7) / 8;  // m-tiles of one XCD's share at most (see xcd_mtile)
   const dim3 grid_gu(8 * per_xcd * ((L.I + GU_COLS - 1) / GU_COLS));
-  // scales in pairs of groups when the rows hold an even number of groups
-  if ((L.H / GROUP) % 2 == 0)
-    KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, true>), grid_gu, dim3(256), 0, s, L, x,
-                c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act);
-  else
-    KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, false>), grid_gu, dim3(256), 0, s, L, x,
-                c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act);
+  // weights from the prefill copy when the layer has one, else the MLX tensors with scales in
+  // pairs of groups when the rows hold an even number of groups
+  const bool pk = L.pk[0].codes != nullptr;
+  const int bl_gu = pk ? 2 : (L.H / GROUP) % 2 == 0 ? 1 : 0;
+  const int bl_dn = pk ? 2 : (L.I / GROUP) % 2 == 0 ? 1 : 0;
+#define KMOE_GU(BLV)                                                                                         \
+  KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, BLV>), grid_gu, dim3(256), 0, s, L, x, \
+              c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act)
+  if (bl_gu == 2) KMOE_GU(2); else if (bl_gu == 1) KMOE_GU(1); else KMOE_GU(0);
+#undef KMOE_GU
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const dim3 grid_dn(8 * per_xcd * ((L.H + DN_COLS - 1) / DN_COLS));
-  const bool sp = (L.I / GROUP) % 2 == 0;
-#define KMOE_DOWN(OUT16, SPV)                                                                                  \
-  KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, OUT16, SPV>), grid_dn, dim3(256), 0, s, L, w.perm, \
+#define KMOE_DOWN(OUT16, BLV)                                                                                  \
+  KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, OUT16, BLV>), grid_dn, dim3(256), 0, s, L, w.perm, \
               w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale,                    \
               OUT16 ? (float*)nullptr : w.y32, OUT16 ? y16 : (uint16_t*)nullptr)
   if (y16) {
-    if (sp) KMOE_DOWN(true, true); else KMOE_DOWN(true, false);
+    if (bl_dn == 2) KMOE_DOWN(true, 2); else if (bl_dn == 1) KMOE_DOWN(true, 1); else KMOE_DOWN(true, 0);
   } else {
-    if (sp) KMOE_DOWN(false, true); else KMOE_DOWN(false, false);
+    if (bl_dn == 2) KMOE_DOWN(false, 2); else if (bl_dn == 1) KMOE_DOWN(false, 1); else KMOE_DOWN(false, 0);
   }
 #undef KMOE_DOWN
   return hipGetLastError();
@@ -562,6 +618,96 @@ hipError_t launch_combine(const float* y32, const uint16_t* y16, const float* wt
                 out32);
   }
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
+// Prefill weight copy.  One wavefront load of the grouped GEMMs reads, per 32-row block and
+// group, the two chunks of each of the 32 rows; in the MLX layout those are 32 separate
+// row-strided pieces, in the copy one contiguous 64-chunk run.  Scales and biases of a group
+// pair of a row sit side by side (s0 s1 b0 b1), one 8-byte load, with an odd last group padded.
+// ---------------------------------------------------------------------------------------------
+
+PackLayout pack_layout(int H, int I, int E, int bits) {
+  PackLayout p{};
+  const int64_t rows[3] = {I, I, H}, in[3] = {H, H, I};
+  auto up256 = [](int64_t v) { return (v + 255) & ~(int64_t)255; };
+  int64_t off = 0;
+  for (int q = 0; q < 3; ++q) {
+    p.codes_expert[q] = rows[q] * in[q] * bits / 8;
+    p.codes[q] = off;
+    off = up256(off + p.codes_expert[q] * E);
+  }
+  for (int q = 0; q < 3; ++q) {
+    const int64_t ng = in[q] / GROUP, npair = (ng + 1) / 2;
+    p.sb_expert[q] = rows[q] * npair * 8;
+    p.sb[q] = off;
+    off = up256(off + p.sb_expert[q] * E);
+  }
+  p.total = off;
+  return p;
+}
+
+// One thread per output chunk o = ((e*nrb + rb)*ng + g)*64 + n + 32h: chunk 2g+h of row 32rb+n.
+template <int BITS>
+__global__ __launch_bounds__(256) void pack_codes_kernel(const QProj P, int rows, int in, int E,
+                                                         uint8_t* __restrict__ dst) {
+  constexpr int CB = Bits<BITS>::chunk_bytes, CD = Bits<BITS>::chunk_dwords;
+  const int ng = in / GROUP, nrb = rows / 32;
+  const size_t o = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= (size_t)E * nrb * ng * 64) return;
+  const int lane = (int)(o & 63);
+  size_t r = o >> 6;
+  const int g = (int)(r % ng);
+  r /= ng;
+  const int rb = (int)(r % nrb), e = (int)(r / nrb);
+  const int row = rb * 32 + (lane & 31), chunk = 2 * g + (lane >> 5);
+  const size_t rbytes = (size_t)in * BITS / 8;
+  const uint32_t* src =
+      reinterpret_cast<const uint32_t*>(P.w + (size_t)e * P.w_stride + row * rbytes + (size_t)chunk * CB);
+  uint32_t* out = reinterpret_cast<uint32_t*>(dst + o * CB);
+#pragma unroll
+  for (int i = 0; i < CD; ++i) out[i] = src[i];
+}
+
+// One thread per (e, rb, pair, n): s[2p] s[2p+1] b[2p] b[2p+1] of row 32rb+n (zeros past ng).
+__global__ __launch_bounds__(256) void pack_sb_kernel(const QProj P, int rows, int in, int E,
+                                                      uint2* __restrict__ dst) {
+  const int ng = in / GROUP, npair = (ng + 1) / 2, nrb = rows / 32;
+  const size_t o = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= (size_t)E * nrb * npair * 32) return;
+  const int n = (int)(o & 31);
+  size_t r = o >> 5;
+  const int pr = (int)(r % npair);
+  r /= npair;
+  const int rb = (int)(r % nrb), e = (int)(r / nrb);
+  const size_t base = (size_t)e * P.s_stride + (size_t)(rb * 32 + n) * ng;
+  const int g0 = 2 * pr, g1 = 2 * pr + 1;
+  const uint32_t s0 = P.s[base + g0], b0 = P.b[base + g0];
+  const uint32_t s1 = g1 < ng ? P.s[base + g1] : 0u, b1 = g1 < ng ? P.b[base + g1] : 0u;
+  dst[o] = make_uint2(s0 | (s1 << 16), b0 | (b1 << 16));
+}
+
+hipError_t launch_prefill_pack(const LayerConfig& c, uint8_t* pack, hipStream_t s) {
+  const LayerArgs& L = c.args;
+  const PackLayout pl = pack_layout(L.H, L.I, L.E, c.bits);
+  const QProj* proj[3] = {&L.gate, &L.up, &L.down};
+  const int rows[3] = {L.I, L.I, L.H}, in[3] = {L.H, L.H, L.I};
+  for (int q = 0; q < 3; ++q) {
+    const size_t nc = (size_t)L.E * (rows[q] / 32) * (in[q] / GROUP) * 64;
+    const dim3 gc((unsigned)((nc + 255) / 256));
+    if (c.bits == 3)
+      KMOE_LAUNCH("pack_codes_kernel", pack_codes_kernel<3>, gc, dim3(256), 0, s, *proj[q], rows[q], in[q], L.E,
+                  pack + pl.codes[q]);
+    else
+      KMOE_LAUNCH("pack_codes_kernel", pack_codes_kernel<4>, gc, dim3(256), 0, s, *proj[q], rows[q], in[q], L.E,
+                  pack + pl.codes[q]);
+    const size_t ns = (size_t)L.E * (rows[q] / 32) * ((in[q] / GROUP + 1) / 2) * 32;
+    KMOE_LAUNCH("pack_sb_kernel", pack_sb_kernel, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, s, *proj[q],
+                rows[q], in[q], L.E, reinterpret_cast<uint2*>(pack + pl.sb[q]));
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
 }
 
 }  // namespace kmoe

@@ -70,11 +70,13 @@ class QuantizedExperts:
 
     Holds the ``kmoe_layer`` handle and a workspace that grows with the largest token
     count seen (allocate it up front with :meth:`reserve` to keep allocation out of
-    timed regions).
+    timed regions).  ``prefill_copy=True`` also keeps the experts in the layout the
+    grouped prefill GEMMs read with whole cache lines (``kmoe_prefill_pack``; about one
+    more copy of the weights); results are the same either way.
     """
 
     def __init__(self, shape: LayerShape, projs: dict, scale_dtype: str = "f16", activation: str = "swiglu",
-                 shared: dict | None = None, keepalive=None):
+                 shared: dict | None = None, keepalive=None, prefill_copy: bool = False):
         if scale_dtype not in ("f16", "bf16"):
             raise ValueError("scale_dtype must be 'f16' or 'bf16'")
         if activation not in ("swiglu", "gelu_tanh"):
@@ -104,8 +106,19 @@ class QuantizedExperts:
             d.shared_up = shared["up"].data_ptr()
             d.shared_down = shared["down"].data_ptr()
             d.shared_intermediate = shape.shared_intermediate
-        self._desc = d
         L = _capi.lib()
+        self._pack = None
+        if prefill_copy:
+            n = ctypes.c_size_t()
+            _capi.check(L.kmoe_prefill_pack_size(ctypes.byref(d), ctypes.byref(n)), "kmoe_prefill_pack_size")
+            pack = torch.empty(n.value, dtype=torch.uint8, device=dev)
+            if pack.data_ptr() % 256:
+                raise RuntimeError("prefill copy allocation is not 256-byte aligned")
+            _capi.check(L.kmoe_prefill_pack(ctypes.byref(d), pack.data_ptr(), n.value, _stream()),
+                        "kmoe_prefill_pack")
+            d.prefill_pack, d.prefill_pack_bytes = pack.data_ptr(), n.value
+            self._pack = pack
+        self._desc = d
         h = ctypes.c_void_p()
         _capi.check(L.kmoe_layer_create(ctypes.byref(d), ctypes.byref(h)), "kmoe_layer_create")
         self._handle = h
@@ -115,7 +128,8 @@ class QuantizedExperts:
     # ---- construction helpers ---------------------------------------------------------
     @classmethod
     def from_stacked(cls, shape: LayerShape, layer: dict, device="cuda", scale_dtype: str = "f16",
-                     activation: str = "swiglu", layout: str = "expert") -> "QuantizedExperts":
+                     activation: str = "swiglu", layout: str = "expert",
+                     prefill_copy: bool = False) -> "QuantizedExperts":
         """From a stacked layer dict (numpy from :func:`synth.make_layer` or torch tensors).
 
         ``layout="expert"`` (default) packs each expert's nine tensors into one contiguous
@@ -145,7 +159,7 @@ class QuantizedExperts:
                 w, s, b = (tensors[(name, k)] for k in ("w", "s", "b"))
                 projs[name] = _Proj(w, _as_u16(s), _as_u16(b), w[0].numel() * w.element_size(),
                                     s[0].numel() * s.element_size())
-            return cls(shape, projs, scale_dtype, activation, shared, list(tensors.values()))
+            return cls(shape, projs, scale_dtype, activation, shared, list(tensors.values()), prefill_copy)
         geom = ExpertGeometry(shape.hidden, shape.intermediate, shape.bits)
         offs, E = geom.offsets(), shape.num_experts
         body = torch.empty((E, geom.expert_size), dtype=torch.uint8, device=device)
@@ -155,10 +169,11 @@ class QuantizedExperts:
                 off = offs[f"{name}_proj.{part}"]
                 body[:, off:off + t.shape[1]] = t
         del tensors
-        return cls(shape, _block_projs(body, geom), scale_dtype, activation, shared, [body])
+        return cls(shape, _block_projs(body, geom), scale_dtype, activation, shared, [body], prefill_copy)
 
     @classmethod
-    def from_bkex(cls, path: str, top_k: int, device="cuda", activation: str | None = None) -> "QuantizedExperts":
+    def from_bkex(cls, path: str, top_k: int, device="cuda", activation: str | None = None,
+                  prefill_copy: bool = False) -> "QuantizedExperts":
         """Load a BKEX ``layer_XX.bin`` file: the expert blocks are uploaded as one buffer and
         described with the block size as expert stride (no repacking).  The activation
         defaults to GELU-tanh for intermediate size 704 and SwiGLU otherwise, as the
@@ -172,7 +187,12 @@ class QuantizedExperts:
         buf = torch.from_numpy(body).to(device)
         shape = LayerShape(hdr.hidden, hdr.intermediate, hdr.num_experts, top_k, hdr.bits)
         act = activation or ("gelu_tanh" if hdr.intermediate == 704 else "swiglu")
-        return cls(shape, _block_projs(buf, geom, hdr.expert_size), hdr.scale_dtype, act, None, [buf])
+        return cls(shape, _block_projs(buf, geom, hdr.expert_size), hdr.scale_dtype, act, None, [buf], prefill_copy)
+
+    def with_prefill_copy(self) -> "QuantizedExperts":
+        """The same experts (sharing these tensors) with a prefill copy made for them."""
+        return QuantizedExperts(self.shape, self.projs, self.scale_dtype, self.activation, self.shared,
+                                self._keepalive, prefill_copy=True)
 
     # ---- workspace --------------------------------------------------------------------
     def workspace_bytes(self, tokens: int) -> int:

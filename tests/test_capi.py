@@ -128,6 +128,36 @@ def test_calls_validate_before_launch():
     L.kmoe_layer_destroy(h)
 
 
+def test_prefill_copy_size_and_validation():
+    L = _capi.lib()
+    n = ctypes.c_size_t()
+    assert L.kmoe_prefill_pack_size(ctypes.byref(_desc()), ctypes.byref(n)) == 0
+    # H=2048, I=512, E=256, 3-bit: 3 x 256 x 512x2048x3/8 code bytes, then per projection
+    # 256 experts x rows x group pairs x 8 bytes (16 pairs x 512 rows; 4 pairs x 2048 rows)
+    assert n.value == 3 * 256 * 393216 + 3 * 256 * 65536
+    # odd group counts are padded to whole pairs: H=320 (5 groups), I=192 (3 groups), E=12
+    d = _desc(hidden=320, intermediate=192, num_experts=12, top_k=3)
+    for p, rows, cols in (("gate", 192, 320), ("up", 192, 320), ("down", 320, 192)):
+        getattr(d, p).weight_expert_stride = rows * cols * 3 // 8
+        getattr(d, p).scale_expert_stride = rows * cols // 64 * 2
+    assert L.kmoe_prefill_pack_size(ctypes.byref(d), ctypes.byref(n)) == 0
+    up = lambda v: (v + 255) // 256 * 256
+    codes = 2 * up(12 * 192 * 320 * 3 // 8) + up(12 * 320 * 192 * 3 // 8)
+    assert n.value == codes + 2 * up(12 * 192 * 3 * 8) + up(12 * 320 * 2 * 8)
+    assert L.kmoe_prefill_pack_size(ctypes.byref(_desc(bits=5)), ctypes.byref(n)) == _capi.ERR_UNSUPPORTED
+    # the copy must be aligned and whole before a layer uses it
+    full = 3 * 256 * 393216 + 3 * 256 * 65536
+    assert _create(_desc(prefill_pack=(1 << 20) + 128, prefill_pack_bytes=full))[0] == _capi.ERR_ALIGNMENT
+    assert _create(_desc(prefill_pack=1 << 20, prefill_pack_bytes=full - 1))[0] == _capi.ERR_INVALID_ARG
+    rc, h = _create(_desc(prefill_pack=1 << 20, prefill_pack_bytes=full))
+    assert rc == 0 and h.value
+    L.kmoe_layer_destroy(h)
+    # kmoe_prefill_pack checks its buffer before launching
+    assert L.kmoe_prefill_pack(ctypes.byref(_desc()), 1 << 20, full - 1, None) == _capi.ERR_INVALID_ARG
+    assert L.kmoe_prefill_pack(ctypes.byref(_desc()), (1 << 20) + 64, full, None) == _capi.ERR_ALIGNMENT
+    assert L.kmoe_prefill_pack(ctypes.byref(_desc()), None, full, None) == _capi.ERR_INVALID_ARG
+
+
 def test_kernel_timing_validates_arguments():
     L = _capi.lib()
     assert L.kmoe_profile_begin(0) == _capi.ERR_INVALID_ARG

@@ -165,6 +165,29 @@ def test_forward_both_weight_layouts(device, layout, T):
         assert np.array_equal(v, layer[k][[3, 0, 11]]), k
 
 
+@pytest.mark.parametrize("name", sorted(SMALL))
+@pytest.mark.parametrize("scale_dtype", ["f16", "bf16"])
+def test_prefill_copy_matches_mlx_layout(device, name, scale_dtype):
+    """The grouped GEMMs give bit-identical layers from the prefill copy and from the MLX
+    tensors (even and odd group counts, both weight layouts); decode sizes are unaffected."""
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+
+    shape = SMALL[name]
+    layer = synth.make_layer(shape, 61, scale_dtype)
+    plain = QuantizedExperts.from_stacked(shape, layer, device, scale_dtype)
+    for layout in ("expert", "stacked"):
+        packed = QuantizedExperts.from_stacked(shape, layer, device, scale_dtype, layout=layout, prefill_copy=True)
+        for T in (3, 9, 300):
+            x, logits = synth.make_inputs(shape, T, 62 + T, zipf=T > 50)
+            xd, ld = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
+            a = SparseMoeBlock(plain)(xd, ld, out_dtype=torch.float32)
+            b = SparseMoeBlock(packed)(xd, ld, out_dtype=torch.float32)
+            assert torch.equal(a, b), f"{name} {scale_dtype} {layout} T={T}"
+            ref = O.moe_layer(layer, x, logits, shape.top_k, shape.bits, scale_dtype=scale_dtype)
+            assert_close(to_np(b), ref["out"], what=f"{name} {scale_dtype} {layout} T={T} prefill copy")
+        assert packed.device_status() == 0
+
+
 def test_kernel_timing_covers_decode_and_prefill(device):
     from kandiga_amd.moe import SparseMoeBlock, profile_kernels
 
@@ -259,6 +282,24 @@ def test_prefill_full_3bit_zipf(device, full3, T, sample):
     rows = np.random.default_rng(T).choice(T, sample, replace=False)
     y = O.switch_mlp(layer, x[rows], ref_idx[rows], 3, nthreads=8)
     assert_close(to_np(out)[rows], O.combine(y, ref_w[rows]), what=f"h2048 3bit prefill T={T}")
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_prefill_copy_full_size(device, full3, bits):
+    """4096-token prefill from the prefill copy equals the MLX-layout result bit for bit."""
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+
+    if bits == 3:
+        shape, layer, plain = full3
+    else:
+        shape = synth.SHAPES["h2048-e256-i512-k8-4bit"]
+        layer = synth.make_layer(shape, 1002)
+        plain = QuantizedExperts.from_stacked(shape, layer, device)
+    packed = QuantizedExperts.from_stacked(shape, layer, device, prefill_copy=True)
+    x, logits = synth.make_inputs(shape, 4096, 3100 + bits, zipf=True)
+    xd, ld = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
+    assert torch.equal(SparseMoeBlock(plain)(xd, ld), SparseMoeBlock(packed)(xd, ld))
+    assert packed.device_status() == 0
 
 
 def test_decode_full_4bit(device):
