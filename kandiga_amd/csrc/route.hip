@@ -36,38 +36,37 @@ __global__ __launch_bounds__(256) void permute_rank_kernel(const int32_t* __rest
                                                            int32_t* __restrict__ local_rank,
                                                            int32_t* __restrict__ tile_hist,
                                                            int32_t* __restrict__ scalars) {
-  extern __shared__ int32_t sm[];
-  int32_t* running = sm;       // [E]
-  int32_t* cnt = sm + E;       // [4][E]
+  // Per round of 256 assignments, lane l of wave w sets bit l of lanes[w][e] for its expert e;
+  // its stable rank in the tile is then the count of its expert so far in earlier rounds, in
+  // waves before w, and in lanes of w below l.
+  extern __shared__ unsigned long long sm64[];
+  unsigned long long* lanes = sm64;                          // [4][E]
+  int32_t* running = reinterpret_cast<int32_t*>(sm64 + 4 * E);  // [E]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int base = blockIdx.x * PERM_TILE;
+  for (int q = tid; q < 4 * E; q += 256) lanes[q] = 0;
   for (int e = tid; e < E; e += 256) running[e] = 0;
+  __syncthreads();
   bool bad = false;
+  const unsigned long long below = (1ull << lane) - 1ull;
   for (int round = 0; round < PERM_TILE / 256; ++round) {
-    for (int q = tid; q < 4 * E; q += 256) cnt[q] = 0;
-    __syncthreads();
     const int a = base + round * 256 + tid;
     int e = a < TK ? idx[a] : -1;
     if (a < TK && (e < 0 || e >= E)) { bad = true; e = -1; }
     const bool valid = e >= 0;
-    uint64_t active = __ballot(valid);
-    int rank_w = 0;
-    while (active) {
-      const int leader = __ffsll((unsigned long long)active) - 1;
-      const int el = __shfl(e, leader, 64);
-      const uint64_t m = __ballot(e == el) & active;
-      if (valid && e == el) rank_w = __popcll(m & ((1ull << lane) - 1ull));
-      if (lane == leader) cnt[wave * E + el] = __popcll(m);
-      active &= ~m;
-    }
+    if (valid) atomicOr(&lanes[wave * E + e], 1ull << lane);
     __syncthreads();
     if (valid) {
-      int pre = running[e];
-      for (int w = 0; w < wave; ++w) pre += cnt[w * E + e];
-      local_rank[a] = pre + rank_w;
+      int pre = running[e] + __popcll(lanes[wave * E + e] & below);
+      for (int w = 0; w < wave; ++w) pre += __popcll(lanes[w * E + e]);
+      local_rank[a] = pre;
     }
     __syncthreads();
-    for (int q = tid; q < E; q += 256) running[q] += cnt[q] + cnt[E + q] + cnt[2 * E + q] + cnt[3 * E + q];
+    for (int q = tid; q < E; q += 256) {
+      running[q] += __popcll(lanes[q]) + __popcll(lanes[E + q]) + __popcll(lanes[2 * E + q]) +
+                    __popcll(lanes[3 * E + q]);
+      lanes[q] = lanes[E + q] = lanes[2 * E + q] = lanes[3 * E + q] = 0;
+    }
     __syncthreads();
   }
   for (int e = tid; e < E; e += 256) tile_hist[(size_t)blockIdx.x * E + e] = running[e];
@@ -115,11 +114,27 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(
   __shared__ int32_t s_off[1024], s_before[1024], s_tot[1024], s_tmp[256];
   const int tid = threadIdx.x, tile = blockIdx.x;
   for (int e = tid; e < E; e += 256) {
-    int tot = 0, before = 0;
-    for (int tt = 0; tt < ntiles; ++tt) {
+    // eight independent partial sums, so the tile counts are loaded back to back
+    int tot8[8] = {}, bef8[8] = {};
+    int tt = 0;
+    for (; tt + 8 <= ntiles; tt += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int h = tile_hist[(size_t)(tt + u) * E + e];
+        bef8[u] += tt + u < tile ? h : 0;
+        tot8[u] += h;
+      }
+    }
+    for (; tt < ntiles; ++tt) {
       const int h = tile_hist[(size_t)tt * E + e];
-      before += tt < tile ? h : 0;
-      tot += h;
+      bef8[0] += tt < tile ? h : 0;
+      tot8[0] += h;
+    }
+    int tot = 0, before = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      tot += tot8[u];
+      before += bef8[u];
     }
     s_tot[e] = tot;
     s_off[e] = tot;
@@ -185,7 +200,8 @@ hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& 
   (void)max_mtiles;
   const int ntiles = (TK + PERM_TILE - 1) / PERM_TILE;
   if (ntiles == 0) return hipSuccess;
-  KMOE_LAUNCH("permute_rank_kernel", permute_rank_kernel, dim3(ntiles), dim3(256), (size_t)5 * E * sizeof(int32_t), s, idx, TK, E,
+  KMOE_LAUNCH("permute_rank_kernel", permute_rank_kernel, dim3(ntiles), dim3(256),
+              (size_t)4 * E * sizeof(unsigned long long) + (size_t)E * sizeof(int32_t), s, idx, TK, E,
                      w.local_rank, w.tile_hist, w.scalars);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
