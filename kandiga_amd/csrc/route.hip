@@ -75,8 +75,9 @@ __global__ __launch_bounds__(256) void permute_rank_kernel(const int32_t* __rest
 
 // In-place exclusive scan of n <= 1024 ints in LDS by a 256-thread block; returns the total.
 __device__ int block_exclusive_scan(int32_t* v, int n, int32_t* tmp) {
-  const int tid = threadIdx.x;
-  // each thread owns up to 4 consecutive entries
+  // n <= 1024: thread t owns entries 4t..4t+3; a shuffle scan per wave, then the four wave
+  // totals through tmp (two barriers in all)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int loc[4], s = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -84,16 +85,17 @@ __device__ int block_exclusive_scan(int32_t* v, int n, int32_t* tmp) {
     loc[j] = i < n ? v[i] : 0;
     s += loc[j];
   }
-  tmp[tid] = s;
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {
-    const int add = tid >= off ? tmp[tid - off] : 0;
-    __syncthreads();
-    tmp[tid] += add;
-    __syncthreads();
+  int incl = s;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += t;
   }
-  const int total = tmp[255];
-  int run = tid > 0 ? tmp[tid - 1] : 0;
+  if (lane == 63) tmp[wave] = incl;
+  __syncthreads();
+  int run = incl - s;
+  for (int w = 0; w < wave; ++w) run += tmp[w];
+  const int total = tmp[0] + tmp[1] + tmp[2] + tmp[3];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = tid * 4 + j;
