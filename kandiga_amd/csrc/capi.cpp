@@ -402,9 +402,8 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
     e = launch_decode(c, d, s);
   } else {
     const int mmt = max_mtiles_for(tokens * K, a.E);
-    e = launch_route(logits, tokens, a.E, K, w.idx, w.wts, s);
+    e = launch_route_xpair(logits, tokens, a.E, K, w.idx, w.wts, xx, a.H, c.bits, w.xpp, s);
     if (e == hipSuccess) e = launch_permute(w.idx, tokens * K, K, a.E, w, mmt, s);
-    if (e == hipSuccess) e = launch_xpair(c, xx, tokens, w.xpp, s);
     if (e == hipSuccess) e = launch_gemm(c, w.xpp, tokens, w, mmt, nullptr, w.wts, s);
     if (e == hipSuccess)
       e = launch_combine(w.y32, nullptr, nullptr, tokens, K, a.H, a.sh_gate ? w.shared_out : nullptr, out, out32,

@@ -183,6 +183,25 @@ __device__ __forceinline__ void load_chunk(const uint8_t* __restrict__ row, int 
 }
 
 // Permute 32 natural-order fp16 values (16 dwords, dword m = elements 2m, 2m+1) into pair order.
+// 32 fp16 values (64 bytes) between memory and registers, as four 16-byte accesses.
+__device__ __forceinline__ void load16g(const void* p, uint32_t (&v)[16]) {
+  const uint4* s = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint4 t = s[q];
+    v[4 * q] = t.x;
+    v[4 * q + 1] = t.y;
+    v[4 * q + 2] = t.z;
+    v[4 * q + 3] = t.w;
+  }
+}
+
+__device__ __forceinline__ void store16s(_Float16* dst, const uint32_t (&v)[16]) {
+  uint4* d = reinterpret_cast<uint4*>(dst);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) d[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+}
+
 template <int BITS>
 __device__ __forceinline__ void to_pair_order(const uint32_t (&nat)[16], uint32_t (&out)[16]) {
 #pragma unroll

@@ -116,6 +116,9 @@ void prof_events(const char* kernel_name, hipStream_t s, hipEvent_t* start, hipE
 
 // ---- launchers (return hipError_t of the launch) ----------------------------------------
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s);
+// launch_route plus xpp = x [T][H] in pair order for `bits`-bit codes (one launch).
+hipError_t launch_route_xpair(const float* logits, int T, int E, int K, int32_t* idx, float* wts, const uint16_t* x,
+                              int H, int bits, uint16_t* xpp, hipStream_t s);
 hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, hipStream_t s);
 hipError_t launch_decode(const LayerConfig& c, const DecodeCall& d, hipStream_t s);
 // x [T][H] -> xpp in pair order (per 32-wide chunk), the gate/up GEMM's A layout.

@@ -54,24 +54,6 @@ __device__ __forceinline__ float activate_p(float g, float u) {
   }
 }
 
-__device__ __forceinline__ void load16g(const void* p, uint32_t (&v)[16]) {
-  const uint4* s = reinterpret_cast<const uint4*>(p);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint4 t = s[q];
-    v[4 * q] = t.x;
-    v[4 * q + 1] = t.y;
-    v[4 * q + 2] = t.z;
-    v[4 * q + 3] = t.w;
-  }
-}
-
-__device__ __forceinline__ void store16s(_Float16* dst, const uint32_t (&v)[16]) {
-  uint4* d = reinterpret_cast<uint4*>(dst);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) d[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-}
-
 __device__ __forceinline__ float16_t mfma32(const half8_t a, const half8_t b, const float16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }

@@ -32,6 +32,27 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 // ---- multi-tile permutation ---------------------------------------------------------------
 // Pass 1: per tile of PERM_TILE assignments, the stable rank of each assignment among the
 // tile's assignments of the same expert, and the tile's expert histogram.
+// Routing plus the pair-order copy of x that the grouped GEMMs read (the GEMM path of the
+// fused layer): the wave that routes token t also rewrites its H/32 chunks of x.
+template <int BITS>
+__global__ __launch_bounds__(256) void route_xpair_kernel(const float* __restrict__ logits, int T, int E, int K,
+                                                          int32_t* __restrict__ idx, float* __restrict__ wts,
+                                                          const uint16_t* __restrict__ x, int H,
+                                                          uint16_t* __restrict__ xpp) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const float* row = logits + (size_t)t * E;
+  int32_t* io = idx + (size_t)t * K;
+  float* wo = wts + (size_t)t * K;
+  KMOE_TOPK_DISPATCH(E, (wave_topk<EPL_>(row, E, K, io, wo, nullptr, nullptr)));
+  for (int c = lane; c < H / CHUNK; c += 64) {
+    uint32_t nat[16], pr[16];
+    load16g(x + (size_t)t * H + c * CHUNK, nat);
+    to_pair_order<BITS>(nat, pr);
+    store16s(reinterpret_cast<_Float16*>(xpp + (size_t)t * H + c * CHUNK), pr);
+  }
+}
+
 __global__ __launch_bounds__(256) void permute_rank_kernel(const int32_t* __restrict__ idx, int TK, int E,
                                                            int32_t* __restrict__ local_rank,
                                                            int32_t* __restrict__ tile_hist,
@@ -194,6 +215,19 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s) {
   if (T == 0) return hipSuccess;
   KMOE_LAUNCH("route_kernel", route_kernel<0>, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, idx, wts);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_xpair(const float* logits, int T, int E, int K, int32_t* idx, float* wts, const uint16_t* x,
+                              int H, int bits, uint16_t* xpp, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  const dim3 grid((T + 3) / 4);
+  if (bits == 3)
+    KMOE_LAUNCH("route_xpair_kernel", route_xpair_kernel<3>, grid, dim3(256), 0, s, logits, T, E, K, idx, wts, x, H,
+                xpp);
+  else
+    KMOE_LAUNCH("route_xpair_kernel", route_xpair_kernel<4>, grid, dim3(256), 0, s, logits, T, E, K, idx, wts, x, H,
+                xpp);
   return hipGetLastError();
 }
 

@@ -200,7 +200,7 @@ def test_kernel_timing_covers_decode_and_prefill(device):
         got = [blk(*a) for a in ins]
     for r, g in zip(ref, got):
         assert torch.equal(r, g)
-    names = ("dec_stage1_kernel", "dec_stage2_kernel", "route_kernel", "permute_rank_kernel",
+    names = ("dec_stage1_kernel", "dec_stage2_kernel", "route_xpair_kernel", "permute_rank_kernel",
              "permute_scatter_kernel", "gemm_gateup_kernel", "gemm_down_kernel", "combine_kernel")
     for n in names:
         assert prof.result[n]["launches"] == 1, n
