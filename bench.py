@@ -61,6 +61,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-shared-layer", dest="shared_layer", action="store_false",
                    help="skip the hidden-2560 layer with the dense shared expert")
+    p.add_argument("--no-wide-prefill", dest="wide_prefill", action="store_false",
+                   help="skip the 4096-token prefill of the hidden-4096 / 512-expert layer")
     p.add_argument("--stack60", action="store_true",
                    help="also run the 60-layer hidden-4096 / 512-expert / top-10 stack (~169 GB resident)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -241,6 +243,21 @@ def main():
                 f"expert bytes)")
         prefill["shared_layer_prefill_T2048"] = prefill_case(ex4[0], shp4, 2048, " (hidden 2560 + shared)")
         del ex4
+        torch.cuda.empty_cache()
+
+    # the hidden-4096 / 512-expert / top-10 layer at 4096 prefill tokens
+    if args.wide_prefill and args.prefill:
+        shp6 = synth.SHAPES["h4096-e512-i1024-k10-3bit"]
+        log(f"generating 1 layer of {shp6.name}")
+        ex6 = QuantizedExperts.from_stacked(shp6, synth.make_layer_torch(shp6, 7300, dev), dev)
+        torch.cuda.synchronize()
+        prefill["wide_layer_prefill_T4096"] = prefill_case(ex6, shp6, 4096, " (hidden 4096, 512 experts, top-10)")
+        if args.prefill_copy:
+            ex6c = ex6.with_prefill_copy()
+            prefill["wide_layer_prefill_copy_T4096"] = prefill_case(
+                ex6c, shp6, 4096, " (hidden 4096, 512 experts, top-10, prefill copy)")
+            del ex6c
+        del ex6
         torch.cuda.empty_cache()
 
     # 60 independent hidden-4096 / 512-expert / top-10 layers resident (~169 GB): one decode

@@ -318,15 +318,20 @@ def test_decode_full_4bit(device):
 
 
 def test_wide_layer_h4096_e512_k10(device):
-    """H=4096, E=512, I=1024, K=10 generated on the device; oracle on the selected experts."""
+    """H=4096, E=512, I=1024, K=10 generated on the device; oracle on the selected experts of
+    sampled rows, up to the 4096-token prefill (also from the prefill copy, bit for bit)."""
     from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
 
     shape = synth.SHAPES["h4096-e512-i1024-k10-3bit"]
     layer_t = synth.make_layer_torch(shape, 5001, device)
     ex = QuantizedExperts.from_stacked(shape, layer_t, device)
-    for T, zipf in ((1, False), (8, False), (300, True)):
+    packed = ex.with_prefill_copy()
+    for T, zipf in ((1, False), (8, False), (300, True), (4096, True)):
         x, logits = synth.make_inputs(shape, T, 5100 + T, zipf=zipf)
-        out = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device))
+        xd, ld = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
+        out = SparseMoeBlock(ex)(xd, ld)
+        if T > 8:
+            assert torch.equal(SparseMoeBlock(packed)(xd, ld), out), f"prefill copy T={T}"
         idx, w = O.route(logits, shape.top_k)
         rows = np.arange(T) if T <= 8 else np.random.default_rng(T).choice(T, 12, replace=False)
         uniq, pos = remap(idx[rows])
