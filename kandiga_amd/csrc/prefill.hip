@@ -98,6 +98,8 @@ __global__ __launch_bounds__(256) void xpair_kernel(const uint16_t* __restrict__
 
 constexpr int LDA = 72;                      // halves per row of the A slab (64 + 8 pad: 144 B)
 constexpr int SLAB = GEMM_BM * LDA;          // halves per slab buffer
+constexpr int EPI_LD = 68;                   // floats per row of a wave's epilogue staging (64 + 4)
+static_assert(4 * 32 * EPI_LD * 4 <= 2 * SLAB * 2, "down epilogue staging must fit in the slabs");
 
 // Workgroup b -> (m-tile, column tile).  Workgroups are dealt to the 8 XCDs round-robin (XCD x
 // runs b = x, x+8, ...).  XCD x takes a contiguous share of the m-tile list (the m-tiles of one
@@ -433,28 +435,38 @@ __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, i
   float16_t acc[4][2];
   zero_acc(acc);
   gemm_mainloop<BITS, BF16, NB, 2, BL>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, R, (int)ng);
-  const int h = lane >> 5;
+  // Epilogue through LDS (the slabs are free once every wave is past the k loop): per 32-row
+  // block the wave writes its 32 x 64 results in the MFMA layout, then reads them back as rows,
+  // so each lane stores 4 consecutive columns of one row (16 bytes fp32, 8 bytes fp16).
+  lds_barrier();
+  float* const wst = reinterpret_cast<float*>(sA) + wave * (32 * EPI_LD);
+  const int h = lane >> 5, n = lane & 31, c4 = 4 * (lane & 15);
 #pragma unroll
   for (int mb = 0; mb < NB; ++mb) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int r = 32 * mb + 8 * (v >> 2) + 4 * h + (v & 3);
-      if (r < nrows) {
-        const size_t ybase = (size_t)s_asg[r] * H;
-        const float wa = s_wa[r];
+      const int rr = 8 * (v >> 2) + 4 * h + (v & 3);
+      wst[rr * EPI_LD + n] = acc[mb][0][v];
+      wst[rr * EPI_LD + 32 + n] = acc[mb][1][v];
+    }
+    asm volatile("" ::: "memory");  // one wave's LDS accesses run in order; keep them in order
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int cb = c0 + 32 * j;
-          if (cb < H) {
-            if constexpr (OUT16) {
-              y16[ybase + cb + (lane & 31)] = f32_to_f16_bits(acc[mb][j][v] * wa);
-            } else {
-              y32[ybase + cb + (lane & 31)] = acc[mb][j][v] * wa;
-            }
-          }
+    for (int i = 0; i < 8; ++i) {
+      const int rr = (lane >> 4) + 4 * i, r = 32 * mb + rr;
+      const float4 q = *reinterpret_cast<const float4*>(wst + rr * EPI_LD + c4);
+      if (r < nrows && c0 < H) {
+        const size_t yo = (size_t)s_asg[r] * H + c0 + c4;
+        const float wa = s_wa[r];
+        if constexpr (OUT16) {
+          const uint32_t lo = (uint32_t)f32_to_f16_bits(q.x * wa) | ((uint32_t)f32_to_f16_bits(q.y * wa) << 16);
+          const uint32_t hi = (uint32_t)f32_to_f16_bits(q.z * wa) | ((uint32_t)f32_to_f16_bits(q.w * wa) << 16);
+          *reinterpret_cast<uint2*>(y16 + yo) = make_uint2(lo, hi);
+        } else {
+          *reinterpret_cast<float4*>(y32 + yo) = make_float4(q.x * wa, q.y * wa, q.z * wa, q.w * wa);
         }
       }
     }
+    asm volatile("" ::: "memory");
   }
 }
 
