@@ -98,7 +98,8 @@ __global__ __launch_bounds__(256) void xpair_kernel(const uint16_t* __restrict__
 
 constexpr int LDA = 72;                      // halves per row of the A slab (64 + 8 pad: 144 B)
 constexpr int SLAB = GEMM_BM * LDA;          // halves per slab buffer
-constexpr int EPI_LD = 68;                   // floats per row of a wave's epilogue staging (64 + 4)
+constexpr int EPI_LD = 68;                   // floats per row of a wave's down epilogue staging (64 + 4)
+constexpr int EPA_LD = 40;                   // halves per row of a wave's gate/up epilogue staging (32 + 8)
 static_assert(4 * 32 * EPI_LD * 4 <= 2 * SLAB * 2, "down epilogue staging must fit in the slabs");
 
 // Workgroup b -> (m-tile, column tile).  Workgroups are dealt to the 8 XCDs round-robin (XCD x
@@ -352,16 +353,27 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
   float16_t acc[4][2];
   zero_acc(acc);
   gemm_mainloop<BITS, BF16, NB, 2, BL>(acc, sA, x + (size_t)tok * H, R, (int)ng);
-  if (c0 >= I) return;
-  const int h = lane >> 5;
-  uint16_t* const ap = act + (size_t)row0 * I + c0 + pairpos_p<BITS>(lane & 31);
+  // Epilogue through LDS (the slabs are free once every wave is past the k loop): per 32-row
+  // block the wave writes its 32 x 32 act values at their pair-order columns, then each lane
+  // stores 8 consecutive columns (16 bytes) of a row.
+  lds_barrier();
+  uint16_t* const wst = reinterpret_cast<uint16_t*>(sA) + wave * (32 * EPA_LD);
+  const int h = lane >> 5, pc = pairpos_p<BITS>(lane & 31), c8 = 8 * (lane & 3);
 #pragma unroll
   for (int mb = 0; mb < NB; ++mb) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int r = 32 * mb + 8 * (v >> 2) + 4 * h + (v & 3);
-      if (r < nrows) ap[(size_t)r * I] = f32_to_f16_bits(activate_p<ACT>(acc[mb][0][v], acc[mb][1][v]));
+      const int rr = 8 * (v >> 2) + 4 * h + (v & 3);
+      wst[rr * EPA_LD + pc] = f32_to_f16_bits(activate_p<ACT>(acc[mb][0][v], acc[mb][1][v]));
     }
+    asm volatile("" ::: "memory");  // one wave's LDS accesses run in order; keep them in order
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int rr = (lane >> 2) + 16 * i, r = 32 * mb + rr;
+      const uint4 q = *reinterpret_cast<const uint4*>(wst + rr * EPA_LD + c8);
+      if (r < nrows && c0 < I) *reinterpret_cast<uint4*>(act + (size_t)(row0 + r) * I + c0 + c8) = q;
+    }
+    asm volatile("" ::: "memory");
   }
 }
 
