@@ -170,7 +170,7 @@ def test_forward_both_weight_layouts(device, layout, T):
 def test_prefill_copy_matches_mlx_layout(device, name, scale_dtype):
     """The grouped GEMMs give bit-identical layers from the prefill copy and from the MLX
     tensors (even and odd group counts, both weight layouts); decode sizes are unaffected."""
-    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+    from kandiga_amd.moe import QuantizedExperts, QuantizedSwitchGLU, SparseMoeBlock
 
     shape = SMALL[name]
     layer = synth.make_layer(shape, 61, scale_dtype)
@@ -185,6 +185,9 @@ def test_prefill_copy_matches_mlx_layout(device, name, scale_dtype):
             assert torch.equal(a, b), f"{name} {scale_dtype} {layout} T={T}"
             ref = O.moe_layer(layer, x, logits, shape.top_k, shape.bits, scale_dtype=scale_dtype)
             assert_close(to_np(b), ref["out"], what=f"{name} {scale_dtype} {layout} T={T} prefill copy")
+            # the switch_mlp contract (per-assignment fp16 outputs) reads the copy too
+            ix = torch.from_numpy(O.route(logits, shape.top_k)[0]).to(device)
+            assert torch.equal(QuantizedSwitchGLU(plain)(xd, ix), QuantizedSwitchGLU(packed)(xd, ix))
         assert packed.device_status() == 0
 
 
