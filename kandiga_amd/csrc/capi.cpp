@@ -65,7 +65,9 @@ void prof_reset() {
   g_prof = Prof{};
 }
 
-int max_mtiles_for(int TK, int E) { return (TK + GEMM_BM - 1) / GEMM_BM + (E < TK ? E : TK); }
+// m-tiles of TK assignments over E experts at bm rows per tile, at most (workspace sizing uses the
+// shorter tiles).
+int max_mtiles_for(int TK, int E, int bm = GEMM_BM_PACK) { return (TK + bm - 1) / bm + (E < TK ? E : TK); }
 
 // Carve the workspace for `T` tokens.  base == nullptr computes the size only.
 Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y, size_t* total) {
@@ -324,7 +326,7 @@ int kmoe_permute(const int32_t* idx, int32_t tokens, int32_t top_k, int32_t num_
     if (e == hipSuccess) e = hipMemsetAsync(num_unique, 0, 4, s);
     return e == hipSuccess ? ok() : hip_fail(e, "permute (empty)");
   }
-  e = launch_permute(idx, TK, top_k, num_experts, w, max_mtiles_for(TK, num_experts), s);
+  e = launch_permute(idx, TK, top_k, num_experts, w, max_mtiles_for(TK, num_experts, GEMM_BM), GEMM_BM, s);
   if (e == hipSuccess) e = hipMemcpyAsync(num_unique, w.scalars, 4, hipMemcpyDeviceToDevice, s);
   return e == hipSuccess ? ok() : hip_fail(e, "permute launch");
 }
@@ -350,8 +352,8 @@ int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, 
     DecodeCall d{xx, nullptr, idx, tokens, nullptr, nullptr, nullptr, &w, yy, 0, false};
     e = launch_decode(c, d, s);
   } else {
-    const int mmt = max_mtiles_for(tokens * K, c.args.E);
-    e = launch_permute(idx, tokens * K, K, c.args.E, w, mmt, s);
+    const int bm = gemm_bm(c.args), mmt = max_mtiles_for(tokens * K, c.args.E, bm);
+    e = launch_permute(idx, tokens * K, K, c.args.E, w, mmt, bm, s);
     if (e == hipSuccess) e = launch_xpair(c, xx, tokens, w.xpp, s);
     if (e == hipSuccess) e = launch_gemm(c, w.xpp, tokens, w, mmt, yy, nullptr, s);
   }
@@ -401,9 +403,9 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
     DecodeCall d{xx, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true};
     e = launch_decode(c, d, s);
   } else {
-    const int mmt = max_mtiles_for(tokens * K, a.E);
+    const int bm = gemm_bm(a), mmt = max_mtiles_for(tokens * K, a.E, bm);
     e = launch_route_xpair(logits, tokens, a.E, K, w.idx, w.wts, xx, a.H, c.bits, w.xpp, s);
-    if (e == hipSuccess) e = launch_permute(w.idx, tokens * K, K, a.E, w, mmt, s);
+    if (e == hipSuccess) e = launch_permute(w.idx, tokens * K, K, a.E, w, mmt, bm, s);
     if (e == hipSuccess) e = launch_gemm(c, w.xpp, tokens, w, mmt, nullptr, w.wts, s);
     if (e == hipSuccess)
       e = launch_combine(w.y32, nullptr, nullptr, tokens, K, a.H, a.sh_gate ? w.shared_out : nullptr, out, out32,

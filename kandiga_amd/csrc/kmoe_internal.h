@@ -75,7 +75,9 @@ struct Work {
 };
 
 constexpr int PERM_TILE = 1024;   // assignments per permutation tile
-constexpr int GEMM_BM = 128;      // assignment rows per grouped-GEMM tile
+constexpr int GEMM_BM = 128;      // assignment rows per grouped-GEMM tile (MLX-layout weights)
+constexpr int GEMM_BM_PACK = 64;  // rows per tile from the prefill copy at hidden <= 2048: half
+                                  // the accumulators, three or four workgroups per CU
 constexpr int DEC_MAX_TOKENS = 8; // largest batch served by the GEMV path
 constexpr int DEC_STAGE2_ASSIGN = 128; // assignments held in two lane slots by decode stage 2
 
@@ -119,7 +121,13 @@ hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, 
 // launch_route plus xpp = x [T][H] in pair order for `bits`-bit codes (one launch).
 hipError_t launch_route_xpair(const float* logits, int T, int E, int K, int32_t* idx, float* wts, const uint16_t* x,
                               int H, int bits, uint16_t* xpp, hipStream_t s);
-hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, hipStream_t s);
+// bm: rows per grouped-GEMM tile of the m-tile list (GEMM_BM, or GEMM_BM_PACK for a layer with
+// the prefill copy; launch_gemm must be called for the same layer).
+hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, int bm,
+                          hipStream_t s);
+// Tiles of 64 rows pay off with the prefill copy's cheap weight loads, up to a gate/up k loop of
+// 2048; past that the 128-row tile's weight reuse wins.
+inline int gemm_bm(const LayerArgs& a) { return a.pk[0].codes && a.H <= 2048 ? GEMM_BM_PACK : GEMM_BM; }
 hipError_t launch_decode(const LayerConfig& c, const DecodeCall& d, hipStream_t s);
 // x [T][H] -> xpp in pair order (per 32-wide chunk), the gate/up GEMM's A layout.
 hipError_t launch_xpair(const LayerConfig& c, const uint16_t* x, int T, uint16_t* xpp, hipStream_t s);

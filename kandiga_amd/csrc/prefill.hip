@@ -54,6 +54,26 @@ __device__ __forceinline__ float activate_p(float g, float u) {
   }
 }
 
+// N dwords (2N halves) of an A row between memory and registers, as 16-byte accesses.
+template <int N>
+__device__ __forceinline__ void stage_load(const void* p, uint32_t (&v)[N]) {
+  const uint4* s = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+  for (int q = 0; q < N / 4; ++q) {
+    const uint4 t = s[q];
+    v[4 * q] = t.x;
+    v[4 * q + 1] = t.y;
+    v[4 * q + 2] = t.z;
+    v[4 * q + 3] = t.w;
+  }
+}
+template <int N>
+__device__ __forceinline__ void stage_store(_Float16* dst, const uint32_t (&v)[N]) {
+  uint4* d = reinterpret_cast<uint4*>(dst);
+#pragma unroll
+  for (int q = 0; q < N / 4; ++q) d[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+}
+
 __device__ __forceinline__ float16_t mfma32(const half8_t a, const half8_t b, const float16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -72,10 +92,11 @@ __global__ __launch_bounds__(256) void xpair_kernel(const uint16_t* __restrict__
 
 // ---- grouped GEMMs ----------------------------------------------------------------------
 // Shared structure of both GEMMs.  A workgroup (4 waves) owns one m-tile: up to GEMM_BM = 128
-// expert-sorted assignment rows of one expert, as four 32-row blocks.  Each wave owns two
-// 32-column blocks of the output for all of the tile's rows, so its 8 accumulator blocks of
-// v_mfma_f32_32x32x16_f16 hold 128 x 64 fp32 values, and two workgroups fit on a CU: while one
-// waits at its k-step barrier or for loads, the other's waves issue.
+// expert-sorted assignment rows of one expert, as four 32-row blocks (64 rows, two blocks, from
+// the prefill copy).  Each wave owns two 32-column blocks of the output for all of the tile's
+// rows, so its 8 accumulator blocks of v_mfma_f32_32x32x16_f16 hold 128 x 64 fp32 values, and
+// two workgroups fit on a CU (three or four with 64-row tiles): while one waits at its k-step
+// barrier or for loads, the others' waves issue.
 //
 //   * A (x rows for gate/up, act rows for down) is shared by the four waves: per 64-wide k step
 //     (one quantization group) the tile's rows are loaded once into an LDS slab (double
@@ -97,10 +118,13 @@ __global__ __launch_bounds__(256) void xpair_kernel(const uint16_t* __restrict__
 // is multiplied.
 
 constexpr int LDA = 72;                      // halves per row of the A slab (64 + 8 pad: 144 B)
-constexpr int SLAB = GEMM_BM * LDA;          // halves per slab buffer
 constexpr int EPI_LD = 68;                   // floats per row of a wave's down epilogue staging (64 + 4)
 constexpr int EPA_LD = 40;                   // halves per row of a wave's gate/up epilogue staging (32 + 8)
-static_assert(4 * 32 * EPI_LD * 4 <= 2 * SLAB * 2, "down epilogue staging must fit in the slabs");
+// LDS of a GEMM workgroup in halves: two A slabs, or the epilogue staging if larger
+constexpr int lds_halves(int bm, bool down) {
+  return 2 * bm * LDA > (down ? 4 * 32 * EPI_LD * 2 : 4 * 32 * EPA_LD) ? 2 * bm * LDA
+                                                                         : (down ? 4 * 32 * EPI_LD * 2 : 4 * 32 * EPA_LD);
+}
 
 // Workgroup b -> (m-tile, column tile).  Workgroups are dealt to the 8 XCDs round-robin (XCD x
 // runs b = x, x+8, ...).  XCD x takes a contiguous share of the m-tile list (the m-tiles of one
@@ -234,15 +258,17 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // weights come from: 0 the MLX tensors with per-group scales; 1 the MLX tensors with scales
 // and biases in pairs of groups (one pair per loop iteration, loaded an iteration ahead; ng
 // even); 2 the prefill copy (pairs padded to even, so ng may be odd).
-template <int BITS, bool BF16, int NB, int JB, int BL>
+template <int BITS, bool BF16, int NB, int JB, int BL, int BM>
 __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16* __restrict__ sA,
                                               const uint16_t* __restrict__ arow, const BRows<JB>& R, int ng) {
   constexpr bool SP = BL >= 1, PK = BL == 2;
+  // thread t stages part t % TPR (HPT halves) of slab row t / TPR
+  constexpr int SLAB = BM * LDA, TPR = 256 / BM, HPT = 64 / TPR;
   const int tid = threadIdx.x, lane = tid & 63;
-  _Float16* const st = sA + (tid >> 1) * LDA + 32 * (tid & 1);
-  const uint16_t* const ag = arow + 32 * (tid & 1);
+  _Float16* const st = sA + (tid / TPR) * LDA + HPT * (tid % TPR);
+  const uint16_t* const ag = arow + HPT * (tid % TPR);
   const int last = ng - 1;
-  uint32_t ar[16];
+  uint32_t ar[HPT / 2];
   BGroup<JB> G0, G1;
   BScalePair<JB> S, Sn;
   uint16_t sc[JB], bi[JB];
@@ -252,9 +278,9 @@ __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16*
     load_scale_pair<JB, PK>(R, 0, S);
     load_scale_pair<JB, PK>(R, min(1, last >> 1), Sn);
   }
-  load16g(ag, ar);
-  store16s(st, ar);
-  load16g(ag + (size_t)min(1, last) * 64, ar);
+  stage_load(ag, ar);
+  stage_store(st, ar);
+  stage_load(ag + (size_t)min(1, last) * 64, ar);
   lds_barrier();
   // pairs of groups (slab 0, then slab 1), so the loop has one exit; an odd last group follows
   int g = 0;
@@ -266,8 +292,8 @@ __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16*
       gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, G0.s, G0.b);
     }
     load_group<BITS, JB, !SP>(R, min(g + 2, last), G0);
-    store16s(st + SLAB, ar);
-    load16g(ag + (size_t)min(g + 2, last) * 64, ar);
+    stage_store(st + SLAB, ar);
+    stage_load(ag + (size_t)min(g + 2, last) * 64, ar);
     lds_barrier();
     if constexpr (SP) {
       pair_half(S, 1, sc, bi);
@@ -280,8 +306,8 @@ __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16*
       S = Sn;
       load_scale_pair<JB, PK>(R, min((g >> 1) + 2, last >> 1), Sn);
     }
-    store16s(st, ar);
-    load16g(ag + (size_t)min(g + 3, last) * 64, ar);
+    stage_store(st, ar);
+    stage_load(ag + (size_t)min(g + 3, last) * 64, ar);
     lds_barrier();
   }
   if (g < ng) {  // an odd last group (scale pairs: the low half of the last, padded pair)
@@ -313,13 +339,13 @@ constexpr int DN_COLS = 4 * 64;  // output columns per down workgroup
 // the 32 columns c0 = 128ct + 32w + n.  Each lane holds matching gate and up values and writes
 // act = silu(gate) * up (fp16, pair order within each 32-column chunk, the down projection's k
 // order) for the sorted position of each row.
-template <int BITS, bool BF16, int ACT, int NB, int BL>
+template <int BITS, bool BF16, int ACT, int NB, int BL, int BM>
 __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* __restrict__ x, int K,
                                             const int32_t* __restrict__ perm, int e, int row0, int nrows, int ct,
                                             _Float16* sA, uint16_t* __restrict__ act) {
   const int H = L.H, I = L.I;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
-  const int lr = tid >> 1;
+  const int lr = tid / (256 / BM);
   const int tok = perm[row0 + min(lr, nrows - 1)] / K;  // rows past the tile's end reload its last row
   const int c0 = ct * GU_COLS + wave * 32;
   const uint32_t rbytes = (uint32_t)H * BITS / 8, ng = (uint32_t)H / GROUP;
@@ -352,7 +378,7 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
   }
   float16_t acc[4][2];
   zero_acc(acc);
-  gemm_mainloop<BITS, BF16, NB, 2, BL>(acc, sA, x + (size_t)tok * H, R, (int)ng);
+  gemm_mainloop<BITS, BF16, NB, 2, BL, BM>(acc, sA, x + (size_t)tok * H, R, (int)ng);
   // Epilogue through LDS (the slabs are free once every wave is past the k loop): per 32-row
   // block the wave writes its 32 x 32 act values at their pair-order columns, then each lane
   // stores 8 consecutive columns (16 bytes) of a row.
@@ -377,23 +403,30 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
   }
 }
 
-template <int BITS, bool BF16, int ACT, int BL>
-__global__ __launch_bounds__(256, 2) void gemm_gateup_kernel(const LayerArgs L, const uint16_t* __restrict__ x,
+// BM rows per tile: 128, or 64 where the shorter tile's 64 accumulators let three gate/up or
+// (down_wgs) up to four down workgroups share a CU.
+template <int BITS, bool BF16, int ACT, int BL, int BM>
+__global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_gateup_kernel(const LayerArgs L, const uint16_t* __restrict__ x,
                                                              int K, const int32_t* __restrict__ perm,
                                                              const int32_t* __restrict__ scalars,
                                                              const int32_t* __restrict__ mt_expert,
                                                              const int32_t* __restrict__ mt_row0,
                                                              const int32_t* __restrict__ mt_rows,
                                                              uint16_t* __restrict__ act) {
-  __shared__ __attribute__((aligned(16))) _Float16 sA[2 * SLAB];
+  __shared__ __attribute__((aligned(16))) _Float16 sA[lds_halves(BM, false)];
   int mt, ct;
   if (!xcd_mtile(blockIdx.x, (L.I + GU_COLS - 1) / GU_COLS, uniform(scalars[1]), mt, ct)) return;
   const int e = uniform(mt_expert[mt]), row0 = uniform(mt_row0[mt]), nrows = uniform(mt_rows[mt]);
-  switch ((nrows + 31) >> 5) {
-    case 1: gateup_tile<BITS, BF16, ACT, 1, BL>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-    case 2: gateup_tile<BITS, BF16, ACT, 2, BL>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-    case 3: gateup_tile<BITS, BF16, ACT, 3, BL>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-    default: gateup_tile<BITS, BF16, ACT, 4, BL>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+  if constexpr (BM == 64) {
+    if (nrows <= 32) gateup_tile<BITS, BF16, ACT, 1, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act);
+    else gateup_tile<BITS, BF16, ACT, 2, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act);
+  } else {
+    switch ((nrows + 31) >> 5) {
+      case 1: gateup_tile<BITS, BF16, ACT, 1, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+      case 2: gateup_tile<BITS, BF16, ACT, 2, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+      case 3: gateup_tile<BITS, BF16, ACT, 3, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+      default: gateup_tile<BITS, BF16, ACT, 4, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+    }
   }
 }
 
@@ -401,14 +434,14 @@ __global__ __launch_bounds__(256, 2) void gemm_gateup_kernel(const LayerArgs L, 
 // c0 + 32j + n with c0 = 256ct + 64w (j = 0, 1).  Row r of the tile (sorted position row0 + r)
 // is written to its assignment perm[row0 + r]: fp16 unweighted (the switch_mlp contract) or fp32
 // scaled by the assignment's routing weight (the fused layer, summed by combine_kernel).
-template <int BITS, bool BF16, bool OUT16, int NB, int BL>
+template <int BITS, bool BF16, bool OUT16, int NB, int BL, int BM>
 __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, int nrows, int ct, _Float16* sA,
                                           const int32_t* s_asg, const float* s_wa,
                                           const uint16_t* __restrict__ act, float* __restrict__ y32,
                                           uint16_t* __restrict__ y16) {
   const int H = L.H, I = L.I;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
-  const int lr = tid >> 1;
+  const int lr = tid / (256 / BM);
   const int c0 = ct * DN_COLS + wave * 64;
   const uint32_t rbytes = (uint32_t)I * BITS / 8, ng = (uint32_t)I / GROUP;
   BRows<2> R;
@@ -446,7 +479,7 @@ __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, i
   }
   float16_t acc[4][2];
   zero_acc(acc);
-  gemm_mainloop<BITS, BF16, NB, 2, BL>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, R, (int)ng);
+  gemm_mainloop<BITS, BF16, NB, 2, BL, BM>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, R, (int)ng);
   // Epilogue through LDS (the slabs are free once every wave is past the k loop): per 32-row
   // block the wave writes its 32 x 64 results in the MFMA layout, then reads them back as rows,
   // so each lane stores 4 consecutive columns of one row (16 bytes fp32, 8 bytes fp16).
@@ -482,8 +515,14 @@ __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, i
   }
 }
 
-template <int BITS, bool BF16, bool OUT16, int BL>
-__global__ __launch_bounds__(256, 2) void gemm_down_kernel(const LayerArgs L, const int32_t* __restrict__ perm,
+// Workgroups per CU of the down GEMM: with 64-row tiles as many as the kernel's registers allow
+// without spilling (4 for 3-bit codes with fp16 scales, 2 for 4-bit codes with bf16 scales, else
+// 3), two with 128-row tiles.
+constexpr int down_wgs(int bits, bool bf16, int bm) {
+  return bm != 64 ? 2 : (bits == 3 && !bf16) ? 4 : (bits == 4 && bf16) ? 2 : 3;
+}
+template <int BITS, bool BF16, bool OUT16, int BL, int BM>
+__global__ __launch_bounds__(256, down_wgs(BITS, BF16, BM)) void gemm_down_kernel(const LayerArgs L, const int32_t* __restrict__ perm,
                                                            const int32_t* __restrict__ scalars,
                                                            const int32_t* __restrict__ mt_expert,
                                                            const int32_t* __restrict__ mt_row0,
@@ -491,29 +530,30 @@ __global__ __launch_bounds__(256, 2) void gemm_down_kernel(const LayerArgs L, co
                                                            const uint16_t* __restrict__ act,
                                                            const float* __restrict__ wscale,
                                                            float* __restrict__ y32, uint16_t* __restrict__ y16) {
-  __shared__ __attribute__((aligned(16))) _Float16 sA[2 * SLAB];
-  __shared__ int32_t s_asg[GEMM_BM];  // assignment of each tile row, and its routing weight
-  __shared__ float s_wa[GEMM_BM];
+  __shared__ __attribute__((aligned(16))) _Float16 sA[lds_halves(BM, true)];
+  __shared__ int32_t s_asg[BM];  // assignment of each tile row, and its routing weight
+  __shared__ float s_wa[BM];
   int mt, ct;
   if (!xcd_mtile(blockIdx.x, (L.H + DN_COLS - 1) / DN_COLS, uniform(scalars[1]), mt, ct)) return;
   const int e = uniform(mt_expert[mt]), row0 = uniform(mt_row0[mt]), nrows = uniform(mt_rows[mt]);
   const int tid = threadIdx.x;
-  if (tid < GEMM_BM) {  // read after the k loop's barriers
+  if (tid < BM) {  // read after the k loop's barriers
     const int a = tid < nrows ? perm[row0 + tid] : 0;
     s_asg[tid] = a;
     s_wa[tid] = wscale && tid < nrows ? wscale[a] : 1.0f;
   }
-  switch ((nrows + 31) >> 5) {
-    case 1: down_tile<BITS, BF16, OUT16, 1, BL>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-    case 2: down_tile<BITS, BF16, OUT16, 2, BL>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-    case 3: down_tile<BITS, BF16, OUT16, 3, BL>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-    default: down_tile<BITS, BF16, OUT16, 4, BL>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+  if constexpr (BM == 64) {
+    if (nrows <= 32) down_tile<BITS, BF16, OUT16, 1, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16);
+    else down_tile<BITS, BF16, OUT16, 2, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16);
+  } else {
+    switch ((nrows + 31) >> 5) {
+      case 1: down_tile<BITS, BF16, OUT16, 1, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+      case 2: down_tile<BITS, BF16, OUT16, 2, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+      case 3: down_tile<BITS, BF16, OUT16, 3, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+      default: down_tile<BITS, BF16, OUT16, 4, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+    }
   }
 }
-
-// out[t, h] = sum_k w[t,k] * y[t*K + k, h] (+ shared[t, h]), fp32 accumulation in k order.
-// Y = float (the fused layer's fp32 rows, already scaled by their routing weights: wts is null)
-// or uint16_t (fp16 bits of switch_mlp outputs, weighted here).
 template <typename Y>
 __global__ __launch_bounds__(256) void combine_kernel(const Y* __restrict__ y, const float* __restrict__ wts, int K,
                                                       int H, const float* __restrict__ shared,
@@ -565,24 +605,31 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
   // weights from the prefill copy when the layer has one, else the MLX tensors with scales in
   // pairs of groups when the rows hold an even number of groups
   const bool pk = L.pk[0].codes != nullptr;
+  const int bm = gemm_bm(L);  // the m-tile list was built with this many rows per tile
   const int bl_gu = pk ? 2 : (L.H / GROUP) % 2 == 0 ? 1 : 0;
   const int bl_dn = pk ? 2 : (L.I / GROUP) % 2 == 0 ? 1 : 0;
-#define KMOE_GU(BLV)                                                                                         \
-  KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, BLV>), grid_gu, dim3(256), 0, s, L, x, \
-              c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act)
-  if (bl_gu == 2) KMOE_GU(2); else if (bl_gu == 1) KMOE_GU(1); else KMOE_GU(0);
+#define KMOE_GU(BLV, BMV)                                                                                    \
+  KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, BLV, BMV>), grid_gu, dim3(256), 0, s, L, \
+              x, c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act)
+  if (bl_gu == 2) {
+    if (bm == 64) KMOE_GU(2, 64); else KMOE_GU(2, 128);
+  } else if (bl_gu == 1) KMOE_GU(1, 128); else KMOE_GU(0, 128);
 #undef KMOE_GU
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const dim3 grid_dn(8 * per_xcd * ((L.H + DN_COLS - 1) / DN_COLS));
-#define KMOE_DOWN(OUT16, BLV)                                                                                  \
-  KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, OUT16, BLV>), grid_dn, dim3(256), 0, s, L, w.perm, \
-              w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale,                    \
+#define KMOE_DOWN(OUT16, BLV, BMV)                                                                              \
+  KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, OUT16, BLV, BMV>), grid_dn, dim3(256), 0, s, L,   \
+              w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale,             \
               OUT16 ? (float*)nullptr : w.y32, OUT16 ? y16 : (uint16_t*)nullptr)
   if (y16) {
-    if (bl_dn == 2) KMOE_DOWN(true, 2); else if (bl_dn == 1) KMOE_DOWN(true, 1); else KMOE_DOWN(true, 0);
+    if (bl_dn == 2) {
+      if (bm == 64) KMOE_DOWN(true, 2, 64); else KMOE_DOWN(true, 2, 128);
+    } else if (bl_dn == 1) KMOE_DOWN(true, 1, 128); else KMOE_DOWN(true, 0, 128);
   } else {
-    if (bl_dn == 2) KMOE_DOWN(false, 2); else if (bl_dn == 1) KMOE_DOWN(false, 1); else KMOE_DOWN(false, 0);
+    if (bl_dn == 2) {
+      if (bm == 64) KMOE_DOWN(false, 2, 64); else KMOE_DOWN(false, 2, 128);
+    } else if (bl_dn == 1) KMOE_DOWN(false, 1, 128); else KMOE_DOWN(false, 0, 128);
   }
 #undef KMOE_DOWN
   return hipGetLastError();

@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(
     const int32_t* __restrict__ tile_hist, int32_t* __restrict__ perm, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ unique, int32_t* __restrict__ ustart,
     int32_t* __restrict__ scalars, int32_t* __restrict__ mt_expert, int32_t* __restrict__ mt_row0,
-    int32_t* __restrict__ mt_rows) {
+    int32_t* __restrict__ mt_rows, int bm) {
   __shared__ int32_t s_off[1024], s_before[1024], s_tot[1024], s_tmp[256];
   const int tid = threadIdx.x, tile = blockIdx.x;
   for (int e = tid; e < E; e += 256) {
@@ -190,18 +190,18 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(
       ustart[s_before[e]] = s_off[e];
     }
   }
-  // grouped-GEMM m-tiles: ceil(count / GEMM_BM) per expert
+  // grouped-GEMM m-tiles: ceil(count / bm) per expert
   __syncthreads();
-  for (int e = tid; e < E; e += 256) s_before[e] = (s_tot[e] + GEMM_BM - 1) / GEMM_BM;
+  for (int e = tid; e < E; e += 256) s_before[e] = (s_tot[e] + bm - 1) / bm;
   __syncthreads();
   const int nmt = block_exclusive_scan(s_before, E, s_tmp);
   for (int e = tid; e < E; e += 256) {
-    const int n = (s_tot[e] + GEMM_BM - 1) / GEMM_BM;
+    const int n = (s_tot[e] + bm - 1) / bm;
     for (int j = 0; j < n; ++j) {
       const int m = s_before[e] + j;
       mt_expert[m] = e;
-      mt_row0[m] = s_off[e] + j * GEMM_BM;
-      mt_rows[m] = min(GEMM_BM, s_tot[e] - j * GEMM_BM);
+      mt_row0[m] = s_off[e] + j * bm;
+      mt_rows[m] = min(bm, s_tot[e] - j * bm);
     }
   }
   if (tid == 0) {
@@ -231,7 +231,8 @@ hipError_t launch_route_xpair(const float* logits, int T, int E, int K, int32_t*
   return hipGetLastError();
 }
 
-hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, hipStream_t s) {
+hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, int bm,
+                          hipStream_t s) {
   (void)K;
   (void)max_mtiles;
   const int ntiles = (TK + PERM_TILE - 1) / PERM_TILE;
@@ -243,7 +244,7 @@ hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& 
   if (err != hipSuccess) return err;
   KMOE_LAUNCH("permute_scatter_kernel", permute_scatter_kernel, dim3(ntiles), dim3(256), 0, s, idx, TK, E, ntiles, w.local_rank,
                      w.tile_hist, w.perm, w.counts, w.offsets, w.unique, w.ustart, w.scalars, w.mt_expert,
-                     w.mt_row0, w.mt_rows);
+                     w.mt_row0, w.mt_rows, bm);
   return hipGetLastError();
 }
 
