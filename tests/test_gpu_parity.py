@@ -191,6 +191,34 @@ def test_prefill_copy_matches_mlx_layout(device, name, scale_dtype):
         assert packed.device_status() == 0
 
 
+TINY = {
+    "h64-i64-e1-k1-3bit": synth.LayerShape(64, 64, 1, 1, 3),
+    "h64-i128-e2-k2-4bit": synth.LayerShape(64, 128, 2, 2, 4),
+    "h128-i64-e3-k2-3bit": synth.LayerShape(128, 64, 3, 2, 3),
+}
+
+
+@pytest.mark.parametrize("name", sorted(TINY))
+def test_tiny_shapes(device, name):
+    """Smallest legal layers: one quantization group per row (odd group counts, padded scale
+    pairs), a single expert with top-1, decode and prefill sizes, with and without the copy."""
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+
+    shape = TINY[name]
+    layer = synth.make_layer(shape, 71)
+    plain = QuantizedExperts.from_stacked(shape, layer, device)
+    packed = QuantizedExperts.from_stacked(shape, layer, device, prefill_copy=True)
+    for T in (1, 5, 8, 9, 77, 300):
+        x, logits = synth.make_inputs(shape, T, 72 + T)
+        xd, ld = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
+        out, idx, _w = SparseMoeBlock(plain)(xd, ld, out_dtype=torch.float32, return_routing=True)
+        ref = O.moe_layer(layer, x, logits, shape.top_k, shape.bits)
+        assert np.array_equal(to_np(idx), ref["idx"]), f"{name} T={T} routing"
+        assert_close(to_np(out), ref["out"], what=f"{name} T={T}")
+        assert torch.equal(SparseMoeBlock(packed)(xd, ld, out_dtype=torch.float32), out), f"{name} T={T} copy"
+    assert plain.device_status() == 0 and packed.device_status() == 0
+
+
 def test_kernel_timing_covers_decode_and_prefill(device):
     from kandiga_amd.moe import SparseMoeBlock, profile_kernels
 
