@@ -9,7 +9,8 @@ different token inputs in turn, so one replay of the captured call sequence touc
 HBM.  A step is one layer call.  Reported beside it: decode at 4 and 8 tokens, the top-4
 "fast mode", and 3-bit prefill of 512/2048/4096 Zipf-routed tokens.
 
-`value` = achieved algorithmic HBM bandwidth of the layer at 1 token, in GB/s:
+`value` = achieved algorithmic HBM bandwidth of the layer at 1 token, in GB/s (with --decode
+lists that leave out 1:8, of the first case measured; `config` then names that case):
 bytes_alg = U*expert_bytes + T*H*2 (x) + T*E*4 (logits) + T*H*2 (out) + T*K*8 (routing),
 U = distinct experts selected, divided by the measured time per layer call.
 
@@ -290,7 +291,9 @@ def main():
                     kernel="dec_stage1_kernel", mean_launch_us=round(head["stage1_us"], 3),
                     bytes_alg_per_launch=round(head["stage1_bytes_alg"]),
                     frac_of_measured_copy=round(head["stage1_gbs"] / copy_gbs, 4))
-        roof["traffic"] = stage1_traffic(head["stage1_bytes_alg"])
+        # the committed counter summary covers the 1-token top-8 workload only
+        if head["T"] == 1 and head["k"] == 8:
+            roof["traffic"] = stage1_traffic(head["stage1_bytes_alg"])
 
     line = {
         "metric": METRIC,
@@ -305,12 +308,13 @@ def main():
         "vs_baseline": None,
         "dtype": "u3",
         "data": "synthetic (seeded MLX-layout 3-bit experts, fp16 scale/bias, fp16 activations; random-init)",
-        "config": {"workload": "moe-layer decode, 1 token, 3-bit top-8, hidden 2048, 256 experts, "
+        "config": {"workload": "moe-layer decode, %d token%s, 3-bit top-%d, hidden 2048, 256 experts, "
                                "intermediate 512, group 64; stack of %d distinct layers, %d inputs per layer"
-                               % (args.layers, head["inputs_per_layer"]),
-                   "tokens": 1, "top_k": shape.top_k, "hidden": H, "experts": E, "intermediate": I,
+                               % (head["T"], "" if head["T"] == 1 else "s", head["k"], args.layers,
+                                  head["inputs_per_layer"]),
+                   "tokens": head["T"], "top_k": head["k"], "hidden": H, "experts": E, "intermediate": I,
                    "bits": 3, "layers_rotated": args.layers},
-        "decode_us_per_token_layer": round(head["us_per_layer"], 3),
+        "decode_us_per_token_layer": round(head["us_per_layer"] / head["T"], 3),
         "roofline": roof,
         "cpu_baseline": cpu,
         "detail": {"measured_copy_GBs": round(copy_gbs, 1),
