@@ -165,6 +165,17 @@ def main():
         r = dict(T=T, k=k, us_per_layer=us, gbs=ba / (us * 1e-6) / 1e9, bytes_alg=ba,
                  unique_experts=sum(uniq) / n, calls=reps * n, inputs_per_layer=P,
                  distinct_expert_bytes_per_replay=distinct)
+        # spread over replays, from a second pass with an event between replays (the events
+        # themselves add a little, so the mean above stays the figure reported)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        ev[0].record()
+        for i in range(reps):
+            run()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        per = sorted(ev[i].elapsed_time(ev[i + 1]) * 1e3 / n for i in range(reps))
+        for name, f in (("us_p10", 0.1), ("us_median", 0.5), ("us_p90", 0.9)):
+            r[name] = per[min(len(per) - 1, int(round(f * (len(per) - 1))))]
         if graph and profile:
             # per-kernel event timing over one eager pass of the same calls
             with profile_kernels(4 * n + 16) as prof:
@@ -189,7 +200,8 @@ def main():
             results[key] = r
             extra = (f"  stage1 {r['stage1_us']:.2f} us ({r['stage1_gbs']:.0f} GB/s) stage2 {r['stage2_us']:.2f} us"
                      if "stage1_us" in r else "")
-            log(f"{key}: {r['us_per_layer']:.2f} us/layer  {r['gbs']:.0f} GB/s  U={r['unique_experts']:.1f} "
+            log(f"{key}: {r['us_per_layer']:.2f} us/layer (replays p10/median/p90 {r['us_p10']:.2f}/"
+                f"{r['us_median']:.2f}/{r['us_p90']:.2f})  {r['gbs']:.0f} GB/s  U={r['unique_experts']:.1f} "
                 f"P={r['inputs_per_layer']} distinct={r['distinct_expert_bytes_per_replay'] / 2**30:.2f} GiB{extra}")
 
     def prefill_case(ex, shp, T, tag=""):
