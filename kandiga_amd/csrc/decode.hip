@@ -317,8 +317,10 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
 // Stage 2.  Lane (g, c) of a wave works on assignment g of its unit and 32-wide chunk c of the
 // intermediate dimension, for RPW consecutive output rows: each act chunk is loaded once per
 // workgroup and reused across the rows.  A unit is (group of 64/LPA assignments, RPW-row
-// subset of the workgroup's S2_ROWS rows); the four waves take units round-robin, UF at a
-// time with all their loads in flight.  Per-assignment row results go to LDS and the combine
+// subset of the workgroup's S2_ROWS rows); the four waves take units round-robin.  With one
+// chunk per lane (intermediate <= 2048) a wave's units form a two-stage pipeline (the next
+// unit's loads in flight while the current one is computed); otherwise UF units at a time
+// have all their loads in flight.  Per-assignment row results go to LDS and the combine
 // sums them in k order (moe_block.metal:515-539), so the result does not depend on timing.
 template <int BITS, bool BF16, int S2_ROWS, int RPW, int UF, bool COMBINE>
 __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int T, int K,
@@ -369,6 +371,95 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int 
   constexpr int NSUB = S2_ROWS / RPW;
   const int nunits = ((TK + AG - 1) / AG) * NSUB;
 
+  if (nchI <= LPA) {
+    // One chunk per lane (intermediate <= 2048): the wave's units (u = wave + 4j) run as a
+    // two-stage pipeline, the loads of unit j+1 in flight while unit j is computed.
+    struct S2Unit {
+      int a, e, hb;
+      bool v;
+    };
+    struct S2Load {
+      uint32_t d[RPW][4], xh[16], xl[16];
+      uint16_t sc[RPW], bi[RPW];
+    };
+    const int c = cl;
+    const bool cv = c < nchI;
+    auto unit_of = [&](int u) {  // uniform control flow (the shuffle needs every lane)
+      S2Unit U;
+      const int grp = u / NSUB;
+      U.hb = h0 + (u - grp * NSUB) * RPW;
+      U.a = grp * AG + g;
+      // the assignment group never straddles the two slots (AG divides 64)
+      const int e = __shfl(grp * AG < 64 ? ev0 : ev1, U.a & 63, 64);
+      U.v = u < nunits && U.a < TK && e >= 0 && e < E;
+      U.e = U.v ? e : 0;
+      return U;
+    };
+    auto load_unit = [&](const S2Unit& U, S2Load& S) {
+      if (U.v && cv) {
+        const uint8_t* wrow = L.down.w + (size_t)U.e * L.down.w_stride + (size_t)U.hb * rbytes;
+        const size_t so = (size_t)U.e * L.down.s_stride + (size_t)U.hb * ng + (c >> 1);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          load_chunk<BITS>(wrow + r * rbytes, c, S.d[r]);
+          S.sc[r] = L.down.s[so + r * ng];
+          S.bi[r] = L.down.b[so + r * ng];
+        }
+        load16(act + (size_t)U.a * I + (size_t)c * CHUNK, S.xh);
+        load16(act + act_plane + (size_t)U.a * I + (size_t)c * CHUNK, S.xl);
+      }
+    };
+    auto finish_unit = [&](int u, const S2Unit& U, const S2Load& S) {
+      float part[RPW];
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) part[r] = 0.f;
+      if (U.v && cv) {
+        float sh = 0.f, sl = 0.f;
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+          sh = fdot2(S.xh[m], ONE2, sh);
+          sl = fdot2(S.xl[m], ONE2, sl);
+        }
+        const float xs = sh + sl;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          uint32_t cp[16];
+          unpack_chunk<BITS, false>(S.d[r], cp);
+          const float sf = scale_to_f32<BF16>(S.sc[r]) * TWO24, bf = scale_to_f32<BF16>(S.bi[r]);
+          part[r] = sf * (chunk_dot(cp, S.xh) + chunk_dot(cp, S.xl)) + bf * xs;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const float v = group_sum_last(part[r], LPA);  // 0 for an assignment with an invalid expert
+        if (cl == LPA - 1 && u < nunits && U.a < TK) {
+          if constexpr (COMBINE) {
+            red[U.a * S2_ROWS + (U.hb - h0) + r] = v;
+          } else {
+            static_cast<uint16_t*>(out)[(size_t)U.a * H + U.hb + r] = f32_to_f16_bits(v);
+          }
+        }
+      }
+    };
+    const int nw = wave < nunits ? (nunits - wave + 3) / 4 : 0;  // this wave's units
+    S2Load S0, S1;
+    S2Unit U0 = unit_of(wave), U1;
+    load_unit(U0, S0);
+    for (int j = 0; j < nw; j += 2) {
+      const int u = wave + 4 * j;
+      if (j + 1 < nw) {
+        U1 = unit_of(u + 4);
+        load_unit(U1, S1);
+      }
+      finish_unit(u, U0, S0);
+      if (j + 1 >= nw) break;
+      if (j + 2 < nw) {
+        U0 = unit_of(u + 8);
+        load_unit(U0, S0);
+      }
+      finish_unit(u + 4, U1, S1);
+    }
+  } else
   for (int u0 = wave; u0 < nunits; u0 += 4 * UF) {
     int av[UF], ea[UF], hb[UF];
     bool va[UF];
