@@ -22,7 +22,9 @@ U*(gate+up bytes of one expert) + T*H*2 + T*E*4 + T*K*I*4 (act written) + T*K*8.
 profiles/ for that kernel and workload (null when absent).
 
 The CPU baseline is the oracle's C restatement of the reference expert MLP (the K experts of
-a token fanned out over threads, as the reference does) timed on this host.
+a token fanned out over threads, as the reference does) timed on this host, with a
+single-thread figure, the host's CPU model and core count, and the 512-token prefill time it
+implies (the reference runs 3-bit prefill as one decode call per token).
 """
 from __future__ import annotations
 
@@ -395,11 +397,29 @@ def cpu_baseline(ex, shape, seconds):
         O.switch_mlp(sub, x[n:n + 1], pos[n:n + 1], shape.bits, nthreads=threads)
         n += 1
     dt = (time.perf_counter() - t0) / n
+    # single-thread figure on a few of the same tokens (about a quarter of the time budget)
+    t1 = time.perf_counter()
+    n1 = 0
+    while n1 < ntok and (time.perf_counter() - t1) < seconds / 4:
+        O.switch_mlp(sub, x[n1:n1 + 1], pos[n1:n1 + 1], shape.bits, nthreads=1)
+        n1 += 1
+    dt1 = (time.perf_counter() - t1) / n1
     ba = shape.top_k * shape.expert_bytes + shape.hidden * 4 + shape.num_experts * 4 + shape.top_k * 8
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     return {"value": round(ba / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{n} decode tokens (1 token x top-8 experts each) of the hidden-2048 3-bit layer, "
                       f"weights resident in RAM; {dt * 1e3:.2f} ms/token",
-            "us_per_token": round(dt * 1e6, 1)}
+            "us_per_token": round(dt * 1e6, 1),
+            "single_thread": {"tokens": n1, "us_per_token": round(dt1 * 1e6, 1),
+                              "GBs": round(ba / dt1 / 1e9, 3)},
+            # the reference runs 3-bit prefill as one decode call per token
+            "prefill_T512_s_extrapolated": round(512 * dt, 3),
+            "host": {"cpu_model": model, "nproc": os.cpu_count()}}
 
 
 if __name__ == "__main__":
