@@ -219,6 +219,30 @@ def test_tiny_shapes(device, name):
     assert plain.device_status() == 0 and packed.device_status() == 0
 
 
+@pytest.mark.parametrize("inter", [512, 1024])
+def test_decode_stage2_unit_counts(device, inter):
+    """Every decode batch (1..8 tokens) at top-K 1, 3, 10, 12 and 16: at intermediate 1024 the
+    down stage gives its waves one to four units each (three included), so every exit of its
+    two-stage unit loop runs.  Fused layer and switch_mlp outputs against the oracle."""
+    from kandiga_amd.moe import QuantizedExperts, QuantizedSwitchGLU, SparseMoeBlock
+
+    base = synth.LayerShape(512, inter, 32, 16, 3)
+    layer = synth.make_layer(base, 81)
+    for K in (1, 3, 10, 12, 16):
+        shape = base.with_top_k(K)
+        ex = QuantizedExperts.from_stacked(shape, layer, device)
+        for T in range(1, 9):
+            x, logits = synth.make_inputs(shape, T, 82 + 10 * T + K)
+            xd, ld = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
+            out, idx, _w = SparseMoeBlock(ex)(xd, ld, out_dtype=torch.float32, return_routing=True)
+            ref = O.moe_layer(layer, x, logits, K, 3)
+            assert np.array_equal(to_np(idx), ref["idx"]), f"I={inter} K={K} T={T} routing"
+            assert_close(to_np(out), ref["out"], what=f"I={inter} K={K} T={T} layer")
+            y = QuantizedSwitchGLU(ex)(xd, torch.from_numpy(ref["idx"]).to(device))
+            assert_close(to_np(y), ref["y"], what=f"I={inter} K={K} T={T} switch_mlp")
+        assert ex.device_status() == 0
+
+
 def test_kernel_timing_covers_decode_and_prefill(device):
     from kandiga_amd.moe import SparseMoeBlock, profile_kernels
 
