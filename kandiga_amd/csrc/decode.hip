@@ -459,76 +459,77 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int 
       }
       finish_unit(u + 4, U1, S1);
     }
-  } else
-  for (int u0 = wave; u0 < nunits; u0 += 4 * UF) {
-    int av[UF], ea[UF], hb[UF];
-    bool va[UF];
-#pragma unroll
-    for (int i = 0; i < UF; ++i) {
-      const int u = u0 + 4 * i;  // uniform
-      const int grp = u / NSUB;
-      hb[i] = h0 + (u - grp * NSUB) * RPW;
-      const int a = grp * AG + g;
-      // the assignment group never straddles the two slots (AG divides 64)
-      const int e = __shfl(grp * AG < 64 ? ev0 : ev1, a & 63, 64);
-      av[i] = a;
-      va[i] = u < nunits && a < TK && e >= 0 && e < E;
-      ea[i] = va[i] ? e : 0;
-    }
-    float part[UF][RPW];
-#pragma unroll
-    for (int i = 0; i < UF; ++i)
-#pragma unroll
-      for (int r = 0; r < RPW; ++r) part[i][r] = 0.f;
-    for (int c = cl; c < nchI; c += LPA) {
-      uint32_t d[UF][RPW][4], xh[UF][16], xl[UF][16];
-      uint16_t sc[UF][RPW], bi[UF][RPW];
+  } else {
+    for (int u0 = wave; u0 < nunits; u0 += 4 * UF) {
+      int av[UF], ea[UF], hb[UF];
+      bool va[UF];
 #pragma unroll
       for (int i = 0; i < UF; ++i) {
-        if (va[i]) {
-          const uint8_t* wrow = L.down.w + (size_t)ea[i] * L.down.w_stride + (size_t)hb[i] * rbytes;
-          const size_t so = (size_t)ea[i] * L.down.s_stride + (size_t)hb[i] * ng + (c >> 1);
+        const int u = u0 + 4 * i;  // uniform
+        const int grp = u / NSUB;
+        hb[i] = h0 + (u - grp * NSUB) * RPW;
+        const int a = grp * AG + g;
+        // the assignment group never straddles the two slots (AG divides 64)
+        const int e = __shfl(grp * AG < 64 ? ev0 : ev1, a & 63, 64);
+        av[i] = a;
+        va[i] = u < nunits && a < TK && e >= 0 && e < E;
+        ea[i] = va[i] ? e : 0;
+      }
+      float part[UF][RPW];
 #pragma unroll
-          for (int r = 0; r < RPW; ++r) {
-            load_chunk<BITS>(wrow + r * rbytes, c, d[i][r]);
-            sc[i][r] = L.down.s[so + r * ng];
-            bi[i][r] = L.down.b[so + r * ng];
+      for (int i = 0; i < UF; ++i)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) part[i][r] = 0.f;
+      for (int c = cl; c < nchI; c += LPA) {
+        uint32_t d[UF][RPW][4], xh[UF][16], xl[UF][16];
+        uint16_t sc[UF][RPW], bi[UF][RPW];
+#pragma unroll
+        for (int i = 0; i < UF; ++i) {
+          if (va[i]) {
+            const uint8_t* wrow = L.down.w + (size_t)ea[i] * L.down.w_stride + (size_t)hb[i] * rbytes;
+            const size_t so = (size_t)ea[i] * L.down.s_stride + (size_t)hb[i] * ng + (c >> 1);
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+              load_chunk<BITS>(wrow + r * rbytes, c, d[i][r]);
+              sc[i][r] = L.down.s[so + r * ng];
+              bi[i][r] = L.down.b[so + r * ng];
+            }
+            load16(act + (size_t)av[i] * I + (size_t)c * CHUNK, xh[i]);
+            load16(act + act_plane + (size_t)av[i] * I + (size_t)c * CHUNK, xl[i]);
           }
-          load16(act + (size_t)av[i] * I + (size_t)c * CHUNK, xh[i]);
-          load16(act + act_plane + (size_t)av[i] * I + (size_t)c * CHUNK, xl[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < UF; ++i) {
+          if (va[i]) {
+            float sh = 0.f, sl = 0.f;
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+              sh = fdot2(xh[i][m], ONE2, sh);
+              sl = fdot2(xl[i][m], ONE2, sl);
+            }
+            const float xs = sh + sl;
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+              uint32_t cp[16];
+              unpack_chunk<BITS, false>(d[i][r], cp);
+              const float sf = scale_to_f32<BF16>(sc[i][r]) * TWO24, bf = scale_to_f32<BF16>(bi[i][r]);
+              part[i][r] += sf * (chunk_dot(cp, xh[i]) + chunk_dot(cp, xl[i])) + bf * xs;
+            }
+          }
         }
       }
 #pragma unroll
       for (int i = 0; i < UF; ++i) {
-        if (va[i]) {
-          float sh = 0.f, sl = 0.f;
+        const int a = av[i];
 #pragma unroll
-          for (int m = 0; m < 16; ++m) {
-            sh = fdot2(xh[i][m], ONE2, sh);
-            sl = fdot2(xl[i][m], ONE2, sl);
-          }
-          const float xs = sh + sl;
-#pragma unroll
-          for (int r = 0; r < RPW; ++r) {
-            uint32_t cp[16];
-            unpack_chunk<BITS, false>(d[i][r], cp);
-            const float sf = scale_to_f32<BF16>(sc[i][r]) * TWO24, bf = scale_to_f32<BF16>(bi[i][r]);
-            part[i][r] += sf * (chunk_dot(cp, xh[i]) + chunk_dot(cp, xl[i])) + bf * xs;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < UF; ++i) {
-      const int a = av[i];
-#pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        const float v = group_sum_last(part[i][r], LPA);  // 0 for an assignment with an invalid expert
-        if (cl == LPA - 1 && u0 + 4 * i < nunits && a < TK) {
-          if constexpr (COMBINE) {
-            red[a * S2_ROWS + (hb[i] - h0) + r] = v;
-          } else {
-            static_cast<uint16_t*>(out)[(size_t)a * H + hb[i] + r] = f32_to_f16_bits(v);
+        for (int r = 0; r < RPW; ++r) {
+          const float v = group_sum_last(part[i][r], LPA);  // 0 for an assignment with an invalid expert
+          if (cl == LPA - 1 && u0 + 4 * i < nunits && a < TK) {
+            if constexpr (COMBINE) {
+              red[a * S2_ROWS + (hb[i] - h0) + r] = v;
+            } else {
+              static_cast<uint16_t*>(out)[(size_t)a * H + hb[i] + r] = f32_to_f16_bits(v);
+            }
           }
         }
       }
