@@ -136,6 +136,16 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(
     int32_t* __restrict__ mt_rows, int bm) {
   __shared__ int32_t s_off[1024], s_before[1024], s_tot[1024], s_tmp[256];
   const int tid = threadIdx.x, tile = blockIdx.x;
+  const int base = tile * PERM_TILE;
+  // the tile's expert ids and ranks are loaded first, in flight with the histogram loads below
+  constexpr int PER_THREAD = PERM_TILE / 256;
+  int32_t ev[PER_THREAD], rk[PER_THREAD];
+#pragma unroll
+  for (int j = 0; j < PER_THREAD; ++j) {
+    const int a = base + tid + 256 * j;
+    ev[j] = a < TK ? idx[a] : -1;
+    rk[j] = a < TK ? local_rank[a] : 0;
+  }
   for (int e = tid; e < E; e += 256) {
     // eight independent partial sums, so the tile counts are loaded back to back
     int tot8[8] = {}, bef8[8] = {};
@@ -165,13 +175,10 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(
   }
   __syncthreads();
   const int total = block_exclusive_scan(s_off, E, s_tmp);
-  const int base = tile * PERM_TILE;
-  for (int i = tid; i < PERM_TILE; i += 256) {
-    const int a = base + i;
-    if (a < TK) {
-      const int e = idx[a];
-      if (e >= 0 && e < E) perm[s_off[e] + s_before[e] + local_rank[a]] = a;
-    }
+#pragma unroll
+  for (int j = 0; j < PER_THREAD; ++j) {
+    const int a = base + tid + 256 * j, e = ev[j];
+    if (a < TK && e >= 0 && e < E) perm[s_off[e] + s_before[e] + rk[j]] = a;
   }
   if (tile != 0) return;
   for (int e = tid; e < E; e += 256) {
