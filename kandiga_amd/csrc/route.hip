@@ -65,14 +65,23 @@ __global__ __launch_bounds__(256) void permute_rank_kernel(const int32_t* __rest
   int32_t* running = reinterpret_cast<int32_t*>(sm64 + 4 * E);  // [E]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int base = blockIdx.x * PERM_TILE;
+  // every round's expert id is loaded up front: one memory round trip instead of one per round
+  constexpr int ROUNDS = PERM_TILE / 256;
+  int32_t ev[ROUNDS];
+#pragma unroll
+  for (int round = 0; round < ROUNDS; ++round) {
+    const int a = base + round * 256 + tid;
+    ev[round] = a < TK ? idx[a] : -1;
+  }
   for (int q = tid; q < 4 * E; q += 256) lanes[q] = 0;
   for (int e = tid; e < E; e += 256) running[e] = 0;
   __syncthreads();
   bool bad = false;
   const unsigned long long below = (1ull << lane) - 1ull;
-  for (int round = 0; round < PERM_TILE / 256; ++round) {
+#pragma unroll
+  for (int round = 0; round < ROUNDS; ++round) {
     const int a = base + round * 256 + tid;
-    int e = a < TK ? idx[a] : -1;
+    int e = ev[round];
     if (a < TK && (e < 0 || e >= E)) { bad = true; e = -1; }
     const bool valid = e >= 0;
     if (valid) atomicOr(&lanes[wave * E + e], 1ull << lane);
