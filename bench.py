@@ -4,27 +4,32 @@
 Workload of the reported value: decode of one token through a 3-bit top-8 MoE layer
 (hidden 2048, 256 experts, intermediate 512, group 64, fp16 scale/bias), over a stack of 8
 distinct seeded layers (2.8 GB of expert weights resident).  Each layer is called with P
-different token inputs in turn, so one replay of the captured call sequence touches more than
-1 GiB of distinct expert bytes (over 4x the 256 MB memory-side cache) and the bytes come from
-HBM.  A step is one layer call.  Reported beside it: decode at 4 and 8 tokens, the top-4
-"fast mode", and 3-bit prefill of 512/2048/4096 Zipf-routed tokens.
+different token inputs in turn, P chosen so that one pass over the call sequence touches at
+least 1 GiB of distinct expert bytes (over 4x the 256 MB memory-side cache), so the bytes come
+from HBM.  A step is one layer call; exactly --steps calls are timed (whole replays of the
+captured sequence plus one captured partial sequence for the remainder).  Beside it: the
+spread over at least 5 replays (at least 200 calls), decode at 4 and 8 tokens, the top-4 "fast
+mode", 4-bit decode (the 4-bit layer of the reference's CPU path), 3-bit prefill of
+512/2048/4096 Zipf-routed tokens, the hidden-2560 layer with its dense shared expert, the
+hidden-4096 / 512-expert / top-10 layer's 4096-token prefill, and one decode token through a
+stack of 60 such layers (169 GB resident).
 
 `value` = achieved algorithmic HBM bandwidth of the layer at 1 token, in GB/s (with --decode
 lists that leave out 1:8, of the first case measured; `config` then names that case):
 bytes_alg = U*expert_bytes + T*H*2 (x) + T*E*4 (logits) + T*H*2 (out) + T*K*8 (routing),
 U = distinct experts selected, divided by the measured time per layer call.
 
-`roofline` is that of the dominant kernel (the decode stage 1: routing, gate/up GEMVs and
-SwiGLU), timed with HIP events around each of its launches (kmoe_profile_begin/end) in an
-eager pass over the same calls; its algorithmic bytes per launch are
-U*(gate+up bytes of one expert) + T*H*2 + T*E*4 + T*K*I*4 (act written) + T*K*8.
-`traffic` comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under
-profiles/ for that kernel and workload (null when absent).
+`roofline` is that of the dominant kernel of the decode call (the one with the largest share of
+its time), timed with HIP events around each of its launches (kmoe_profile_begin/end) in an
+eager pass over the same calls, with the algorithmic bytes per launch of that kernel.
+`traffic` comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under profiles/
+for that kernel and workload (null when absent).
 
-The CPU baseline is the oracle's C restatement of the reference expert MLP (the K experts of
-a token fanned out over threads, as the reference does) timed on this host, with a
-single-thread figure, the host's CPU model and core count, and the 512-token prefill time it
-implies (the reference runs 3-bit prefill as one decode call per token).
+The CPU baseline restates the reference's portable scalar expert MLP (its non-NEON loops, at
+the reference build's -O2 with the host's instruction set; oracle/ref_scalar.c), the K experts
+of a token spread over an OpenMP team as the reference spreads them over GCD, timed on this
+host: the 3-bit decode layer and the 4-bit one.  The oracle's own C restatement (the
+checker: NEON accumulation order, no contraction) is reported beside it.
 """
 from __future__ import annotations
 
@@ -38,9 +43,14 @@ import time
 METRIC = "MoE-layer decode µs/token + HBM GB/s; prefill tokens/s (3-bit, top-8)"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
-ROTATE_BYTES = 1.1 * 2 ** 30   # distinct expert bytes touched per replay of the decode sequence
+ROTATE_BYTES = 1.05 * 2 ** 30  # distinct expert bytes touched per pass over the decode sequence
 HERE = os.path.dirname(os.path.abspath(__file__))
-TRAFFIC_FILE = os.path.join(HERE, "profiles", "dec_stage1_kernel_decode_t1_k8_traffic.json")
+PROFILES = os.path.join(HERE, "profiles")
+
+
+def traffic_file(kernel: str) -> str:
+    """Counter summary of `kernel` at the headline workload (decode, 1 token, top-8)."""
+    return os.path.join(PROFILES, f"{kernel}_decode_t1_k8_traffic.json")
 
 
 def log(msg: str) -> None:
@@ -66,8 +76,10 @@ def parse():
                    help="skip the hidden-2560 layer with the dense shared expert")
     p.add_argument("--no-wide-prefill", dest="wide_prefill", action="store_false",
                    help="skip the 4096-token prefill of the hidden-4096 / 512-expert layer")
-    p.add_argument("--stack60", action="store_true",
-                   help="also run the 60-layer hidden-4096 / 512-expert / top-10 stack (~169 GB resident)")
+    p.add_argument("--no-stack60", dest="stack60", action="store_false",
+                   help="skip the 60-layer hidden-4096 / 512-expert / top-10 decode stack (~169 GB resident)")
+    p.add_argument("--no-4bit", dest="four_bit", action="store_false",
+                   help="skip the 4-bit decode layer (GPU and CPU)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 5 device copies of 256 MiB (the known-size kernel that the "
                         "FETCH_SIZE / WRITE_SIZE counters are calibrated against) and exit")
@@ -106,90 +118,123 @@ def main():
     copy_gbs = measured_copy_gbs(torch, dev)
     log(f"device copy: {copy_gbs:.0f} GB/s (read + write)")
 
-    def decode_case(T, k, graph, exs=None, shp=None, profile=True):
+    def kernel_bytes(name, shp, T, k, U):
+        """Algorithmic bytes of one launch of a decode-path kernel."""
+        H, E, I = shp.hidden, shp.num_experts, shp.intermediate
+        gu = 2 * I * H * shp.bits // 8 + 4 * I * (H // 64) * 2
+        dn = H * I * shp.bits // 8 + 2 * H * (I // 64) * 2
+        act = T * k * I * 4
+        if name == "dec_stage1_kernel":
+            return U * gu + T * H * 2 + T * E * 4 + act + T * k * 8
+        if name == "dec_stage2_kernel":
+            return U * dn + act + T * H * 2 + T * k * 8
+        return U * shp.expert_bytes + T * H * 2 + T * E * 4 + T * H * 2 + T * k * 8
+
+    def decode_case(T, k, graph, exs=None, shp=None, profile=True, steps=None):
         exs = exs if exs is not None else experts[k]
         shp = shp or shape
+        steps = args.steps if steps is None else steps
         H, E, I = shp.hidden, shp.num_experts, shp.intermediate
-        gu_bytes = 2 * I * H * shp.bits // 8 + 4 * I * (H // 64) * 2
         blocks = [SparseMoeBlock(ex) for ex in exs]
         for ex in exs:
             ex.reserve(T)
-        L = len(blocks)
-        est = min(T * k, E) * shp.expert_bytes
-        P = max(1 if L >= 32 else 2, math.ceil(ROTATE_BYTES / (L * est)))
-        seq = []  # (block, x, logits) in call order: every layer with input set 0, then set 1, ...
-        for p in range(P):
+        # Input sets are added until one pass over the sequence touches ROTATE_BYTES of distinct
+        # expert weights (counted from the routing itself): every layer with input set 0, then 1, ...
+        seq, uniq, seen = [], [], [set() for _ in blocks]
+        p = 0
+        while p < 64:
             for li, b in enumerate(blocks):
                 x, lg = synth.make_inputs_torch(shp, T, 9000 + 997 * p + 31 * li + T, dev)
+                _o, idx, _w = b(x, lg, return_routing=True)
+                ids = torch.unique(idx).tolist()
+                seen[li].update(ids)
+                uniq.append(len(ids))
                 seq.append((li, b, x, lg))
-        b_alg, b_s1, uniq, seen = [], [], [], [set() for _ in blocks]
-        for li, b, x, lg in seq:
-            _o, idx, _w = b(x, lg, return_routing=True)
-            ids = torch.unique(idx).tolist()
-            U = len(ids)
-            seen[li].update(ids)
-            uniq.append(U)
-            b_alg.append(U * shp.expert_bytes + shp.shared_bytes + T * H * 2 + T * E * 4 + T * H * 2 + T * k * 8)
-            b_s1.append(U * gu_bytes + T * H * 2 + T * E * 4 + T * k * I * 4 + T * k * 8)
-        distinct = sum(len(s) for s in seen) * shp.expert_bytes
-        outs = [None] * len(seq)
+            p += 1
+            if sum(len(q) for q in seen) * shp.expert_bytes >= ROTATE_BYTES:
+                break
+        P = p
+        n = len(seq)
+        distinct = sum(len(q) for q in seen) * shp.expert_bytes
+        b_alg = [U * shp.expert_bytes + shp.shared_bytes + T * H * 2 + T * E * 4 + T * H * 2 + T * k * 8
+                 for U in uniq]
+        outs = [None] * n
         if graph:
-            g = torch.cuda.CUDAGraph()
+            def capture(calls):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for i, (_li, b, x, lg) in enumerate(calls):
+                        outs[i] = b(x, lg)
+                return g
             s = torch.cuda.Stream()
             s.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(s):
-                for i, (_li, b, x, lg) in enumerate(seq):
-                    outs[i] = b(x, lg)
+                for _li, b, x, lg in seq:
+                    b(x, lg)
             torch.cuda.current_stream().wait_stream(s)
-            with torch.cuda.graph(g):
+            g_full = capture(seq)
+            r = steps % n
+            g_rem = capture(seq[:r]) if r else None
+
+            def run_full():
+                g_full.replay()
+
+            def run_steps():
+                for _ in range(steps // n):
+                    g_full.replay()
+                if g_rem is not None:
+                    g_rem.replay()
+        else:
+            def run_full():
                 for i, (_li, b, x, lg) in enumerate(seq):
                     outs[i] = b(x, lg)
 
-            def run():
-                g.replay()
-        else:
-            def run():
-                for i, (_li, b, x, lg) in enumerate(seq):
-                    outs[i] = b(x, lg)
-        n = len(seq)
+            def run_steps():
+                for j in range(steps):
+                    _li, b, x, lg = seq[j % n]
+                    b(x, lg)
         for _ in range(max(1, math.ceil(args.warmup / n))):
-            run()
-        reps = max(1, args.steps // n)
+            run_full()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(reps):
-            run()
+        run_steps()          # exactly `steps` layer calls
         e1.record()
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * n)
-        ba = sum(b_alg) / n
-        r = dict(T=T, k=k, us_per_layer=us, gbs=ba / (us * 1e-6) / 1e9, bytes_alg=ba,
-                 unique_experts=sum(uniq) / n, calls=reps * n, inputs_per_layer=P,
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        # bytes of the timed calls: full passes plus the first `steps % n` calls
+        timed_bytes = (steps // n) * sum(b_alg) + sum(b_alg[:steps % n])
+        ba = timed_bytes / steps
+        r = dict(T=T, k=k, us_per_layer=us, gbs=ba / (us * 1e-6) / 1e9, bytes_alg=ba, steps=steps,
+                 unique_experts=sum(uniq) / n, calls_per_replay=n, inputs_per_layer=P,
                  distinct_expert_bytes_per_replay=distinct)
-        # spread over replays, from a second pass with an event between replays (the events
-        # themselves add a little, so the mean above stays the figure reported)
+        # spread: at least 5 replays and 200 calls, an event between replays (the events add a
+        # little, so the exact-steps figure above stays the one reported)
+        reps = max(5, math.ceil(200 / n))
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
         ev[0].record()
         for i in range(reps):
-            run()
+            run_full()
             ev[i + 1].record()
         torch.cuda.synchronize()
         per = sorted(ev[i].elapsed_time(ev[i + 1]) * 1e3 / n for i in range(reps))
+        r["spread"] = {"replays": reps, "calls": reps * n}
         for name, f in (("us_p10", 0.1), ("us_median", 0.5), ("us_p90", 0.9)):
             r[name] = per[min(len(per) - 1, int(round(f * (len(per) - 1))))]
         if graph and profile:
             # per-kernel event timing over one eager pass of the same calls
-            with profile_kernels(4 * n + 16) as prof:
+            with profile_kernels(8 * n + 16) as prof:
                 for _li, b, x, lg in seq:
                     b(x, lg)
-            s1 = prof.result.get("dec_stage1_kernel")
-            s2 = prof.result.get("dec_stage2_kernel")
-            if s1 and s2:
-                r["stage1_us"] = s1["mean_ms"] * 1e3
-                r["stage2_us"] = s2["mean_ms"] * 1e3
-                r["stage1_bytes_alg"] = sum(b_s1) / n
-                r["stage1_gbs"] = r["stage1_bytes_alg"] / (s1["mean_ms"] * 1e-3) / 1e9
+            kern = {}
+            Umean = sum(uniq) / n
+            for name, v in prof.result.items():
+                ab = sum(kernel_bytes(name, shp, T, k, U) for U in uniq) / n
+                kern[name] = {"mean_us": v["mean_ms"] * 1e3, "launches": v["launches"], "bytes_alg": ab,
+                              "gbs": ab / (v["mean_ms"] * 1e-3) / 1e9}
+            r["kernels"] = kern
+            r["dominant_kernel"] = max(kern, key=lambda nm: kern[nm]["mean_us"]) if kern else None
+            del Umean
         return r
 
     results = {}
@@ -200,11 +245,11 @@ def main():
             r = decode_case(T, k, graph)
             key = f"decode_T{T}_K{k}_{'graph' if graph else 'eager'}"
             results[key] = r
-            extra = (f"  stage1 {r['stage1_us']:.2f} us ({r['stage1_gbs']:.0f} GB/s) stage2 {r['stage2_us']:.2f} us"
-                     if "stage1_us" in r else "")
-            log(f"{key}: {r['us_per_layer']:.2f} us/layer (replays p10/median/p90 {r['us_p10']:.2f}/"
-                f"{r['us_median']:.2f}/{r['us_p90']:.2f})  {r['gbs']:.0f} GB/s  U={r['unique_experts']:.1f} "
-                f"P={r['inputs_per_layer']} distinct={r['distinct_expert_bytes_per_replay'] / 2**30:.2f} GiB{extra}")
+            extra = "".join(f"  {nm} {v['mean_us']:.2f} us ({v['gbs']:.0f} GB/s)" for nm, v in r.get("kernels", {}).items())
+            log(f"{key}: {r['us_per_layer']:.2f} us/layer over {r['steps']} calls (replays p10/median/p90 "
+                f"{r['us_p10']:.2f}/{r['us_median']:.2f}/{r['us_p90']:.2f})  {r['gbs']:.0f} GB/s  "
+                f"U={r['unique_experts']:.1f} P={r['inputs_per_layer']} "
+                f"distinct={r['distinct_expert_bytes_per_replay'] / 2**30:.2f} GiB{extra}")
 
     def prefill_case(ex, shp, T, tag=""):
         blk = SparseMoeBlock(ex)
@@ -283,12 +328,28 @@ def main():
         ex5 = [QuantizedExperts.from_stacked(shp5, synth.make_layer_torch(shp5, 7200 + i, dev), dev)
                for i in range(60)]
         torch.cuda.synchronize()
-        r = decode_case(1, 10, True, ex5, shp5, profile=False)
+        r = decode_case(1, 10, True, ex5, shp5, profile=False, steps=max(args.steps, 60))
         r["us_per_token_60_layers"] = r["us_per_layer"] * 60
         results["stack60_decode_T1_K10_graph"] = r
         log(f"60-layer {shp5.name} stack, decode T=1: {r['us_per_layer']:.2f} us/layer, "
             f"{r['us_per_layer'] * 60:.1f} us/token, {r['gbs']:.0f} GB/s")
         del ex5
+        torch.cuda.empty_cache()
+
+    # the 4-bit layer of the reference's CPU path (hidden 2048, 256 experts, intermediate 512,
+    # top-8): decode of one token on the GPU over a rotated stack, like the 3-bit headline
+    shp1 = synth.SHAPES["h2048-e256-i512-k8-4bit"]
+    if args.four_bit and args.decode:
+        experts.clear()
+        torch.cuda.empty_cache()
+        log(f"generating {args.layers} layers of {shp1.name}")
+        ex1 = [QuantizedExperts.from_stacked(shp1, synth.make_layer_torch(shp1, 7400 + i, dev), dev)
+               for i in range(args.layers)]
+        torch.cuda.synchronize()
+        r = decode_case(1, 8, True, ex1, shp1, profile=False)
+        results["4bit_decode_T1_K8_graph"] = r
+        log(f"{shp1.name} decode T=1: {r['us_per_layer']:.2f} us/layer  {r['gbs']:.0f} GB/s")
+        del ex1
         torch.cuda.empty_cache()
 
     head = results.get("decode_T1_K8_graph") or next(iter(results.values()), None)
@@ -297,24 +358,25 @@ def main():
         return 0
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(experts[8][0], shape, args.cpu_seconds)
+        cpu = cpu_baseline(shape, args.cpu_seconds, shp1 if args.four_bit else None)
 
     roof = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None, "traffic": None}
-    if "stage1_us" in head:
-        roof.update(achieved=round(head["stage1_gbs"], 1), frac=round(head["stage1_gbs"] / HBM_PEAK_GBS, 4),
-                    kernel="dec_stage1_kernel", mean_launch_us=round(head["stage1_us"], 3),
-                    bytes_alg_per_launch=round(head["stage1_bytes_alg"]),
-                    frac_of_measured_copy=round(head["stage1_gbs"] / copy_gbs, 4))
-        # the committed counter summary covers the 1-token top-8 workload only
+    dk = head.get("dominant_kernel")
+    if dk:
+        kv = head["kernels"][dk]
+        roof.update(achieved=round(kv["gbs"], 1), frac=round(kv["gbs"] / HBM_PEAK_GBS, 4), kernel=dk,
+                    mean_launch_us=round(kv["mean_us"], 3), bytes_alg_per_launch=round(kv["bytes_alg"]),
+                    frac_of_measured_copy=round(kv["gbs"] / copy_gbs, 4))
+        # the committed counter summaries cover the 1-token top-8 workload only
         if head["T"] == 1 and head["k"] == 8:
-            roof["traffic"] = stage1_traffic(head["stage1_bytes_alg"])
+            roof["traffic"] = kernel_traffic(dk)
 
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": head["calls"],
+        "steps": head["steps"],
         "warmup": args.warmup,
         "ms_per_step": round(head["us_per_layer"] / 1e3, 6),
         "higher_is_better": True,
@@ -360,12 +422,12 @@ def measured_copy_gbs(torch, dev) -> float:
     return gbs
 
 
-def stage1_traffic(bytes_alg: float):
-    """HBM bytes per launch of the decode stage 1 from the committed rocprofv3 counter summary:
+def kernel_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from its committed rocprofv3 counter summary:
     (FETCH_SIZE + WRITE_SIZE) KiB per dispatch, each divided by the ratio the same counter
-    reads for a device copy of known size."""
+    reads for a device copy of known size (null when there is no summary for the kernel)."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(traffic_file(kernel)) as f:
             t = json.load(f)
         fetch = t["fetch_kib_per_dispatch"] * 1024 / t["copy_fetch_ratio"]
         write = t["write_kib_per_dispatch"] * 1024 / t["copy_write_ratio"]
@@ -374,8 +436,22 @@ def stage1_traffic(bytes_alg: float):
         return None
 
 
-def cpu_baseline(ex, shape, seconds):
-    """Oracle C restatement of the reference expert MLP on this host's cores (T=1, K=8)."""
+def _cpu_time(fn, ntok, seconds):
+    """Mean seconds per token of fn(i) over up to ntok tokens or `seconds` of wall time."""
+    fn(0)  # warm
+    t0 = time.perf_counter()
+    n = 0
+    while n < ntok and (time.perf_counter() - t0) < seconds:
+        fn(n)
+        n += 1
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_baseline(shape, seconds, shape4=None):
+    """The reference's portable scalar expert MLP (oracle/ref_scalar.c) on this host's cores, decode
+    of one token at top-8: the 3-bit layer of the headline (its value) and, with shape4, the
+    4-bit layer.  Experts are generated on the host (16 per layer: the work per token does not
+    depend on which experts are picked); the oracle's checker restatement is timed beside it."""
     import numpy as np
 
     sys.path.insert(0, HERE)
@@ -384,39 +460,43 @@ def cpu_baseline(ex, shape, seconds):
 
     threads = min(shape.top_k, os.cpu_count() or 1, 16)
     ntok = 64
-    x, logits = synth.make_inputs(shape, ntok, 424242)
-    idx, w = O.route(logits, shape.top_k)
-    uniq, inv = np.unique(idx, return_inverse=True)
-    sub = ex.host_subset(uniq.astype(np.int64))
-    pos = inv.reshape(idx.shape).astype(np.int32)
-    log(f"cpu baseline: oracle expert MLP, {threads} threads, up to {seconds:.0f} s")
-    O.switch_mlp(sub, x[:1], pos[:1], shape.bits, nthreads=threads)  # warm
-    t0 = time.perf_counter()
-    n = 0
-    while n < ntok and (time.perf_counter() - t0) < seconds:
-        O.switch_mlp(sub, x[n:n + 1], pos[n:n + 1], shape.bits, nthreads=threads)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    # single-thread figure on a few of the same tokens (about a quarter of the time budget)
-    t1 = time.perf_counter()
-    n1 = 0
-    while n1 < ntok and (time.perf_counter() - t1) < seconds / 4:
-        O.switch_mlp(sub, x[n1:n1 + 1], pos[n1:n1 + 1], shape.bits, nthreads=1)
-        n1 += 1
-    dt1 = (time.perf_counter() - t1) / n1
-    ba = shape.top_k * shape.expert_bytes + shape.hidden * 4 + shape.num_experts * 4 + shape.top_k * 8
+
+    def one(shp, seed, budget):
+        sub_shape = synth.LayerShape(shp.hidden, shp.intermediate, 16, shp.top_k, shp.bits)
+        layer = synth.make_layer(sub_shape, seed, "bf16")   # bf16 scales, as the reference stores them
+        x, logits = synth.make_inputs(sub_shape, ntok, seed + 1)
+        idx, _w = O.route(logits, shp.top_k)
+        dt, n = _cpu_time(lambda i: O.ref_scalar_switch_mlp(layer, x[i:i + 1], idx[i:i + 1], shp.bits, "bf16",
+                                                            nthreads=threads), ntok, budget)
+        dt1, n1 = _cpu_time(lambda i: O.ref_scalar_switch_mlp(layer, x[i:i + 1], idx[i:i + 1], shp.bits, "bf16",
+                                                              nthreads=1), ntok, budget / 4)
+        dto, no = _cpu_time(lambda i: O.switch_mlp(layer, x[i:i + 1], idx[i:i + 1], shp.bits, "bf16",
+                                                   nthreads=threads), ntok, budget / 4)
+        ba = shp.top_k * shp.expert_bytes + shp.hidden * 4 + shp.num_experts * 4 + shp.top_k * 8
+        return ba, dict(tokens=n, us_per_token=round(dt * 1e6, 1), GBs=round(ba / dt / 1e9, 3),
+                        single_thread={"tokens": n1, "us_per_token": round(dt1 * 1e6, 1),
+                                       "GBs": round(ba / dt1 / 1e9, 3)},
+                        checker_restatement={"tokens": no, "us_per_token": round(dto * 1e6, 1),
+                                             "GBs": round(ba / dto / 1e9, 3)})
+
+    log(f"cpu baseline: reference scalar expert MLP, {threads} threads, about {seconds * 1.5:.0f} s per layer")
+    ba, r3 = one(shape, 424242, seconds)
+    r4 = one(shape4, 434343, seconds / 2)[1] if shape4 is not None else None
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
             model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
     except OSError:
         pass
-    return {"value": round(ba / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode tokens (1 token x top-8 experts each) of the hidden-2048 3-bit layer, "
-                      f"weights resident in RAM; {dt * 1e3:.2f} ms/token",
-            "us_per_token": round(dt * 1e6, 1),
-            "single_thread": {"tokens": n1, "us_per_token": round(dt1 * 1e6, 1),
-                              "GBs": round(ba / dt1 / 1e9, 3)},
+    dt = r3["us_per_token"] * 1e-6
+    return {"value": r3["GBs"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{r3['tokens']} decode tokens (1 token x top-8 experts each) of the hidden-2048 3-bit layer, "
+                      f"weights resident in RAM; {dt * 1e3:.2f} ms/token; the reference's scalar loops at -O2 "
+                      f"(oracle/ref_scalar.c), {threads}-thread OpenMP team",
+            "us_per_token": r3["us_per_token"],
+            "single_thread": r3["single_thread"],
+            "checker_restatement": r3["checker_restatement"],
+            "layer_4bit": r4,
             # the reference runs 3-bit prefill as one decode call per token
             "prefill_T512_s_extrapolated": round(512 * dt, 3),
             "host": {"cpu_model": model, "nproc": os.cpu_count()}}

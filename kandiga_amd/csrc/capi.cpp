@@ -356,6 +356,7 @@ int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, 
     e = launch_permute(idx, tokens * K, K, c.args.E, w, mmt, bm, s);
     if (e == hipSuccess) e = launch_xpair(c, xx, tokens, w.xpp, s);
     if (e == hipSuccess) e = launch_gemm(c, w.xpp, tokens, w, mmt, yy, nullptr, s);
+    if (e == hipSuccess) e = launch_zero_bad_rows(idx, tokens * K, c.args.E, c.args.H, yy, s);
   }
   return e == hipSuccess ? ok() : hip_fail(e, "expert_mlp launch");
 }

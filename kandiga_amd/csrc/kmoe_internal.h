@@ -135,6 +135,8 @@ hipError_t launch_xpair(const LayerConfig& c, const uint16_t* x, int T, uint16_t
 // null, Work::y32 (fp32, each row scaled by its routing weight in wscale for the combine).
 hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Work& w, int max_mtiles,
                        uint16_t* y16, const float* wscale, hipStream_t s);
+// y[a] (fp16 [TK][H]) = 0 for every assignment a whose idx[a] lies outside [0, E).
+hipError_t launch_zero_bad_rows(const int32_t* idx, int TK, int E, int H, uint16_t* y, hipStream_t s);
 // out[t] = sum_k (wts ? wts[t,k] : 1) * y[t,k] (+ shared[t]); y is fp32 (y32) or fp16 bits (y16).
 hipError_t launch_combine(const float* y32, const uint16_t* y16, const float* wts, int T, int K, int H,
                           const float* shared, void* out, int out32, hipStream_t s);

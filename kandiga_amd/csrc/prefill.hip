@@ -7,10 +7,14 @@
 //
 //   xpair_kernel: x into pair order once per call (the k order the dequantized weights have).
 //   gemm_gateup_kernel: one workgroup per (m-tile of <= 128 sorted assignments of one expert,
-//     256 intermediate columns of both gate and up); SwiGLU in registers, act written once
-//     (fp16, pair order for the down projection's k dimension).
+//     256 intermediate columns of both gate and up); SwiGLU in registers, act written once as
+//     two fp16 planes, hi = fp16(a) and lo = fp16(a - hi) (about 22 significant bits; pair order
+//     for the down projection's k dimension).
 //   gemm_down_kernel: one workgroup per (m-tile, 512 output columns); A = act rows of the tile
-//     (contiguous, pair order).  The output row of sorted position p is written to assignment
+//     (contiguous, pair order), both planes: each dequantized weight fragment meets the hi and
+//     the lo fragment of the rows, so the down projection sees fp32-quality activations (one
+//     fp16 plane alone is off by up to 2^-12 of |act| per element, which reached 2.7e-2 of
+//     output on 4-bit layers).  The output row of sorted position p is written to assignment
 //     perm[p]: fp16 for the switch_mlp contract, or fp32 scaled by that assignment's routing
 //     weight for the fused layer (an fp16 intermediate would add up to half an fp16 ulp of
 //     each term before the combine).
@@ -120,10 +124,12 @@ __global__ __launch_bounds__(256) void xpair_kernel(const uint16_t* __restrict__
 constexpr int LDA = 72;                      // halves per row of the A slab (64 + 8 pad: 144 B)
 constexpr int EPI_LD = 68;                   // floats per row of a wave's down epilogue staging (64 + 4)
 constexpr int EPA_LD = 40;                   // halves per row of a wave's gate/up epilogue staging (32 + 8)
-// LDS of a GEMM workgroup in halves: two A slabs, or the epilogue staging if larger
+// LDS of a GEMM workgroup in halves: two stages of A slabs (one plane for gate/up, the hi and
+// lo planes for down), or the epilogue staging if larger
 constexpr int lds_halves(int bm, bool down) {
-  return 2 * bm * LDA > (down ? 4 * 32 * EPI_LD * 2 : 4 * 32 * EPA_LD) ? 2 * bm * LDA
-                                                                         : (down ? 4 * 32 * EPI_LD * 2 : 4 * 32 * EPA_LD);
+  return (down ? 4 : 2) * bm * LDA > (down ? 4 * 32 * EPI_LD * 2 : 4 * 32 * EPA_LD)
+             ? (down ? 4 : 2) * bm * LDA
+             : (down ? 4 * 32 * EPI_LD * 2 : 4 * 32 * EPA_LD);
 }
 
 // Workgroup b -> (m-tile, column tile).  Workgroups are dealt to the 8 XCDs round-robin (XCD x
@@ -199,29 +205,54 @@ __device__ __forceinline__ void load_scale_pair(const BRows<JB>& R, int p, BScal
   }
 }
 
-// k16 step ST of one group: A fragments of the NB active row blocks from the slab, B fragments
-// of the JB column blocks dequantized from the group's codes.
-template <int BITS, int NB, int JB, int ST>
+// k16 step ST of one group: A fragments of the NB active row blocks from the slab (NP planes,
+// plane p at slab + p*BM*LDA), B fragments of the JB column blocks dequantized from the group's
+// codes; each B fragment is multiplied by every plane's A fragment.
+template <int BITS, int NB, int JB, int ST, int NP, int BM>
 __device__ __forceinline__ void gemm_step(float16_t (&acc)[4][JB], const _Float16* __restrict__ slab, int lane,
                                           const BGroup<JB>& G, const half2_t (&s2)[JB], const half2_t (&b2)[JB]) {
   const _Float16* ap = slab + (lane & 31) * LDA + 32 * (lane >> 5) + 8 * ST;
-  half8_t af[NB];
+  if constexpr (NP == 1) {
+    half8_t af[NB];
 #pragma unroll
-  for (int mb = 0; mb < NB; ++mb) af[mb] = *reinterpret_cast<const half8_t*>(ap + 32 * mb * LDA);
+    for (int mb = 0; mb < NB; ++mb) af[mb] = *reinterpret_cast<const half8_t*>(ap + 32 * mb * LDA);
 #pragma unroll
-  for (int j = 0; j < JB; ++j) {
-    const u32x4_t q = {dequant_pair(chunk_pair<BITS, 4 * ST + 0, true>(G.d[j]), s2[j], b2[j]),
-                       dequant_pair(chunk_pair<BITS, 4 * ST + 1, true>(G.d[j]), s2[j], b2[j]),
-                       dequant_pair(chunk_pair<BITS, 4 * ST + 2, true>(G.d[j]), s2[j], b2[j]),
-                       dequant_pair(chunk_pair<BITS, 4 * ST + 3, true>(G.d[j]), s2[j], b2[j])};
-    const half8_t bf = __builtin_bit_cast(half8_t, q);
+    for (int j = 0; j < JB; ++j) {
+      const u32x4_t q = {dequant_pair(chunk_pair<BITS, 4 * ST + 0, true>(G.d[j]), s2[j], b2[j]),
+                         dequant_pair(chunk_pair<BITS, 4 * ST + 1, true>(G.d[j]), s2[j], b2[j]),
+                         dequant_pair(chunk_pair<BITS, 4 * ST + 2, true>(G.d[j]), s2[j], b2[j]),
+                         dequant_pair(chunk_pair<BITS, 4 * ST + 3, true>(G.d[j]), s2[j], b2[j])};
+      const half8_t bf = __builtin_bit_cast(half8_t, q);
 #pragma unroll
-    for (int mb = 0; mb < NB; ++mb) acc[mb][j] = mfma32(af[mb], bf, acc[mb][j]);
+      for (int mb = 0; mb < NB; ++mb) acc[mb][j] = mfma32(af[mb], bf, acc[mb][j]);
+    }
+  } else {
+    // the JB B fragments are dequantized once, then each plane's A fragments are read and
+    // multiplied in turn (one plane's fragments live at a time)
+    half8_t bf[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const u32x4_t q = {dequant_pair(chunk_pair<BITS, 4 * ST + 0, true>(G.d[j]), s2[j], b2[j]),
+                         dequant_pair(chunk_pair<BITS, 4 * ST + 1, true>(G.d[j]), s2[j], b2[j]),
+                         dequant_pair(chunk_pair<BITS, 4 * ST + 2, true>(G.d[j]), s2[j], b2[j]),
+                         dequant_pair(chunk_pair<BITS, 4 * ST + 3, true>(G.d[j]), s2[j], b2[j])};
+      bf[j] = __builtin_bit_cast(half8_t, q);
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      half8_t af[NB];
+#pragma unroll
+      for (int mb = 0; mb < NB; ++mb) af[mb] = *reinterpret_cast<const half8_t*>(ap + p * BM * LDA + 32 * mb * LDA);
+#pragma unroll
+      for (int j = 0; j < JB; ++j)
+#pragma unroll
+        for (int mb = 0; mb < NB; ++mb) acc[mb][j] = mfma32(af[mb], bf[j], acc[mb][j]);
+    }
   }
 }
 
 // One group: sc/bi are the rows' scale and bias bits.
-template <int BITS, bool BF16, int NB, int JB>
+template <int BITS, bool BF16, int NB, int JB, int NP, int BM>
 __device__ __forceinline__ void gemm_group(float16_t (&acc)[4][JB], const _Float16* __restrict__ slab, int lane,
                                            const BGroup<JB>& G, const uint16_t (&sc)[JB], const uint16_t (&bi)[JB]) {
   half2_t s2[JB], b2[JB];
@@ -231,10 +262,10 @@ __device__ __forceinline__ void gemm_group(float16_t (&acc)[4][JB], const _Float
     s2[j] = (half2_t){sf, sf};
     b2[j] = (half2_t){bf, bf};
   }
-  gemm_step<BITS, NB, JB, 0>(acc, slab, lane, G, s2, b2);
-  gemm_step<BITS, NB, JB, 1>(acc, slab, lane, G, s2, b2);
-  gemm_step<BITS, NB, JB, 2>(acc, slab, lane, G, s2, b2);
-  gemm_step<BITS, NB, JB, 3>(acc, slab, lane, G, s2, b2);
+  gemm_step<BITS, NB, JB, 0, NP, BM>(acc, slab, lane, G, s2, b2);
+  gemm_step<BITS, NB, JB, 1, NP, BM>(acc, slab, lane, G, s2, b2);
+  gemm_step<BITS, NB, JB, 2, NP, BM>(acc, slab, lane, G, s2, b2);
+  gemm_step<BITS, NB, JB, 3, NP, BM>(acc, slab, lane, G, s2, b2);
 }
 
 template <int JB>
@@ -252,23 +283,33 @@ __device__ __forceinline__ void pair_half(const BScalePair<JB>& S, int hi, uint1
 // across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// The k loop over ng groups.  Thread t stages half (t & 1) of slab row t >> 1 from arow (a row
-// of ng*64 halves).  Every load is unconditional (past the last group the index is clamped,
-// re-reading that group), so the wait counts before each use are exact.  BL selects where the
-// weights come from: 0 the MLX tensors with per-group scales; 1 the MLX tensors with scales
-// and biases in pairs of groups (one pair per loop iteration, loaded an iteration ahead; ng
-// even); 2 the prefill copy (pairs padded to even, so ng may be odd).
-template <int BITS, bool BF16, int NB, int JB, int BL, int BM>
+// The k loop over ng groups.  Thread t stages part of slab row t / TPR from arow (a row of
+// ng*64 halves; with NP = 2 planes also from arow + plane, into the second plane slab).  Every
+// load is unconditional (past the last group the index is clamped, re-reading that group), so
+// the wait counts before each use are exact.  BL selects where the weights come from: 0 the MLX
+// tensors with per-group scales; 1 the MLX tensors with scales and biases in pairs of groups
+// (one pair per loop iteration, loaded an iteration ahead; ng even); 2 the prefill copy (pairs
+// padded to even, so ng may be odd).
+template <int BITS, bool BF16, int NB, int JB, int BL, int BM, int NP>
 __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16* __restrict__ sA,
-                                              const uint16_t* __restrict__ arow, const BRows<JB>& R, int ng) {
+                                              const uint16_t* __restrict__ arow, size_t plane, const BRows<JB>& R,
+                                              int ng) {
   constexpr bool SP = BL >= 1, PK = BL == 2;
   // thread t stages part t % TPR (HPT halves) of slab row t / TPR
-  constexpr int SLAB = BM * LDA, TPR = 256 / BM, HPT = 64 / TPR;
+  constexpr int SLAB = NP * BM * LDA, TPR = 256 / BM, HPT = 64 / TPR;
   const int tid = threadIdx.x, lane = tid & 63;
   _Float16* const st = sA + (tid / TPR) * LDA + HPT * (tid % TPR);
   const uint16_t* const ag = arow + HPT * (tid % TPR);
   const int last = ng - 1;
-  uint32_t ar[HPT / 2];
+  uint32_t ar[NP][HPT / 2];
+  auto a_load = [&](int g) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) stage_load(ag + p * plane + (size_t)g * 64, ar[p]);
+  };
+  auto a_store = [&](_Float16* dst) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) stage_store(dst + p * BM * LDA, ar[p]);
+  };
   BGroup<JB> G0, G1;
   BScalePair<JB> S, Sn;
   uint16_t sc[JB], bi[JB];
@@ -278,44 +319,44 @@ __device__ __forceinline__ void gemm_mainloop(float16_t (&acc)[4][JB], _Float16*
     load_scale_pair<JB, PK>(R, 0, S);
     load_scale_pair<JB, PK>(R, min(1, last >> 1), Sn);
   }
-  stage_load(ag, ar);
-  stage_store(st, ar);
-  stage_load(ag + (size_t)min(1, last) * 64, ar);
+  a_load(0);
+  a_store(st);
+  a_load(min(1, last));
   lds_barrier();
   // pairs of groups (slab 0, then slab 1), so the loop has one exit; an odd last group follows
   int g = 0;
   for (; g + 1 < ng; g += 2) {
     if constexpr (SP) {
       pair_half(S, 0, sc, bi);
-      gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, sc, bi);
+      gemm_group<BITS, BF16, NB, JB, NP, BM>(acc, sA, lane, G0, sc, bi);
     } else {
-      gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, G0.s, G0.b);
+      gemm_group<BITS, BF16, NB, JB, NP, BM>(acc, sA, lane, G0, G0.s, G0.b);
     }
     load_group<BITS, JB, !SP>(R, min(g + 2, last), G0);
-    stage_store(st + SLAB, ar);
-    stage_load(ag + (size_t)min(g + 2, last) * 64, ar);
+    a_store(st + SLAB);
+    a_load(min(g + 2, last));
     lds_barrier();
     if constexpr (SP) {
       pair_half(S, 1, sc, bi);
-      gemm_group<BITS, BF16, NB>(acc, sA + SLAB, lane, G1, sc, bi);
+      gemm_group<BITS, BF16, NB, JB, NP, BM>(acc, sA + SLAB, lane, G1, sc, bi);
     } else {
-      gemm_group<BITS, BF16, NB>(acc, sA + SLAB, lane, G1, G1.s, G1.b);
+      gemm_group<BITS, BF16, NB, JB, NP, BM>(acc, sA + SLAB, lane, G1, G1.s, G1.b);
     }
     load_group<BITS, JB, !SP>(R, min(g + 3, last), G1);
     if constexpr (SP) {
       S = Sn;
       load_scale_pair<JB, PK>(R, min((g >> 1) + 2, last >> 1), Sn);
     }
-    stage_store(st, ar);
-    stage_load(ag + (size_t)min(g + 3, last) * 64, ar);
+    a_store(st);
+    a_load(min(g + 3, last));
     lds_barrier();
   }
   if (g < ng) {  // an odd last group (scale pairs: the low half of the last, padded pair)
     if constexpr (SP) {
       pair_half(S, 0, sc, bi);
-      gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, sc, bi);
+      gemm_group<BITS, BF16, NB, JB, NP, BM>(acc, sA, lane, G0, sc, bi);
     } else {
-      gemm_group<BITS, BF16, NB>(acc, sA, lane, G0, G0.s, G0.b);
+      gemm_group<BITS, BF16, NB, JB, NP, BM>(acc, sA, lane, G0, G0.s, G0.b);
     }
   }
 }
@@ -342,7 +383,7 @@ constexpr int DN_COLS = 4 * 64;  // output columns per down workgroup
 template <int BITS, bool BF16, int ACT, int NB, int BL, int BM>
 __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* __restrict__ x, int K,
                                             const int32_t* __restrict__ perm, int e, int row0, int nrows, int ct,
-                                            _Float16* sA, uint16_t* __restrict__ act) {
+                                            _Float16* sA, uint16_t* __restrict__ act, size_t plane) {
   const int H = L.H, I = L.I;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
   const int lr = tid / (256 / BM);
@@ -378,28 +419,35 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
   }
   float16_t acc[4][2];
   zero_acc(acc);
-  gemm_mainloop<BITS, BF16, NB, 2, BL, BM>(acc, sA, x + (size_t)tok * H, R, (int)ng);
+  gemm_mainloop<BITS, BF16, NB, 2, BL, BM, 1>(acc, sA, x + (size_t)tok * H, 0, R, (int)ng);
   // Epilogue through LDS (the slabs are free once every wave is past the k loop): per 32-row
-  // block the wave writes its 32 x 32 act values at their pair-order columns, then each lane
-  // stores 8 consecutive columns (16 bytes) of a row.
+  // block and plane (hi, then lo) the wave writes its 32 x 32 act values at their pair-order
+  // columns, then each lane stores 8 consecutive columns (16 bytes) of a row.
   lds_barrier();
   uint16_t* const wst = reinterpret_cast<uint16_t*>(sA) + wave * (32 * EPA_LD);
   const int h = lane >> 5, pc = pairpos_p<BITS>(lane & 31), c8 = 8 * (lane & 3);
 #pragma unroll
   for (int mb = 0; mb < NB; ++mb) {
+    float a[16];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int rr = 8 * (v >> 2) + 4 * h + (v & 3);
-      wst[rr * EPA_LD + pc] = f32_to_f16_bits(activate_p<ACT>(acc[mb][0][v], acc[mb][1][v]));
-    }
-    asm volatile("" ::: "memory");  // one wave's LDS accesses run in order; keep them in order
+    for (int v = 0; v < 16; ++v) a[v] = activate_p<ACT>(acc[mb][0][v], acc[mb][1][v]);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int rr = (lane >> 2) + 16 * i, r = 32 * mb + rr;
-      const uint4 q = *reinterpret_cast<const uint4*>(wst + rr * EPA_LD + c8);
-      if (r < nrows && c0 < I) *reinterpret_cast<uint4*>(act + (size_t)(row0 + r) * I + c0 + c8) = q;
+    for (int pl = 0; pl < 2; ++pl) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int rr = 8 * (v >> 2) + 4 * h + (v & 3);
+        const _Float16 hi = (_Float16)a[v];
+        wst[rr * EPA_LD + pc] = pl == 0 ? __builtin_bit_cast(uint16_t, hi) : f32_to_f16_bits(a[v] - (float)hi);
+      }
+      asm volatile("" ::: "memory");  // one wave's LDS accesses run in order; keep them in order
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int rr = (lane >> 2) + 16 * i, r = 32 * mb + rr;
+        const uint4 q = *reinterpret_cast<const uint4*>(wst + rr * EPA_LD + c8);
+        if (r < nrows && c0 < I) *reinterpret_cast<uint4*>(act + pl * plane + (size_t)(row0 + r) * I + c0 + c8) = q;
+      }
+      asm volatile("" ::: "memory");
     }
-    asm volatile("" ::: "memory");
   }
 }
 
@@ -412,20 +460,20 @@ __global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_gateup_kernel(cons
                                                              const int32_t* __restrict__ mt_expert,
                                                              const int32_t* __restrict__ mt_row0,
                                                              const int32_t* __restrict__ mt_rows,
-                                                             uint16_t* __restrict__ act) {
+                                                             uint16_t* __restrict__ act, size_t plane) {
   __shared__ __attribute__((aligned(16))) _Float16 sA[lds_halves(BM, false)];
   int mt, ct;
   if (!xcd_mtile(blockIdx.x, (L.I + GU_COLS - 1) / GU_COLS, uniform(scalars[1]), mt, ct)) return;
   const int e = uniform(mt_expert[mt]), row0 = uniform(mt_row0[mt]), nrows = uniform(mt_rows[mt]);
   if constexpr (BM == 64) {
-    if (nrows <= 32) gateup_tile<BITS, BF16, ACT, 1, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act);
-    else gateup_tile<BITS, BF16, ACT, 2, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act);
+    if (nrows <= 32) gateup_tile<BITS, BF16, ACT, 1, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane);
+    else gateup_tile<BITS, BF16, ACT, 2, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane);
   } else {
     switch ((nrows + 31) >> 5) {
-      case 1: gateup_tile<BITS, BF16, ACT, 1, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-      case 2: gateup_tile<BITS, BF16, ACT, 2, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-      case 3: gateup_tile<BITS, BF16, ACT, 3, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
-      default: gateup_tile<BITS, BF16, ACT, 4, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act); break;
+      case 1: gateup_tile<BITS, BF16, ACT, 1, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane); break;
+      case 2: gateup_tile<BITS, BF16, ACT, 2, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane); break;
+      case 3: gateup_tile<BITS, BF16, ACT, 3, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane); break;
+      default: gateup_tile<BITS, BF16, ACT, 4, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane); break;
     }
   }
 }
@@ -437,7 +485,7 @@ __global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_gateup_kernel(cons
 template <int BITS, bool BF16, bool OUT16, int NB, int BL, int BM>
 __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, int nrows, int ct, _Float16* sA,
                                           const int32_t* s_asg, const float* s_wa,
-                                          const uint16_t* __restrict__ act, float* __restrict__ y32,
+                                          const uint16_t* __restrict__ act, size_t plane, float* __restrict__ y32,
                                           uint16_t* __restrict__ y16) {
   const int H = L.H, I = L.I;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
@@ -479,7 +527,8 @@ __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, i
   }
   float16_t acc[4][2];
   zero_acc(acc);
-  gemm_mainloop<BITS, BF16, NB, 2, BL, BM>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, R, (int)ng);
+  gemm_mainloop<BITS, BF16, NB, 2, BL, BM, 2>(acc, sA, act + (size_t)(row0 + min(lr, nrows - 1)) * I, plane, R,
+                                              (int)ng);
   // Epilogue through LDS (the slabs are free once every wave is past the k loop): per 32-row
   // block the wave writes its 32 x 64 results in the MFMA layout, then reads them back as rows,
   // so each lane stores 4 consecutive columns of one row (16 bytes fp32, 8 bytes fp16).
@@ -516,10 +565,10 @@ __device__ __forceinline__ void down_tile(const LayerArgs& L, int e, int row0, i
 }
 
 // Workgroups per CU of the down GEMM: with 64-row tiles as many as the kernel's registers allow
-// without spilling (4 for 3-bit codes with fp16 scales, 2 for 4-bit codes with bf16 scales, else
-// 3), two with 128-row tiles.
+// without spilling (3: the hi and lo A fragments need more than a quarter of the register file),
+// two with 128-row tiles.
 constexpr int down_wgs(int bits, bool bf16, int bm) {
-  return bm != 64 ? 2 : (bits == 3 && !bf16) ? 4 : (bits == 4 && bf16) ? 2 : 3;
+  return bm != 64 ? 2 : 3;
 }
 template <int BITS, bool BF16, bool OUT16, int BL, int BM>
 __global__ __launch_bounds__(256, down_wgs(BITS, BF16, BM)) void gemm_down_kernel(const LayerArgs L, const int32_t* __restrict__ perm,
@@ -527,7 +576,7 @@ __global__ __launch_bounds__(256, down_wgs(BITS, BF16, BM)) void gemm_down_kerne
                                                            const int32_t* __restrict__ mt_expert,
                                                            const int32_t* __restrict__ mt_row0,
                                                            const int32_t* __restrict__ mt_rows,
-                                                           const uint16_t* __restrict__ act,
+                                                           const uint16_t* __restrict__ act, size_t plane,
                                                            const float* __restrict__ wscale,
                                                            float* __restrict__ y32, uint16_t* __restrict__ y16) {
   __shared__ __attribute__((aligned(16))) _Float16 sA[lds_halves(BM, true)];
@@ -543,14 +592,14 @@ __global__ __launch_bounds__(256, down_wgs(BITS, BF16, BM)) void gemm_down_kerne
     s_wa[tid] = wscale && tid < nrows ? wscale[a] : 1.0f;
   }
   if constexpr (BM == 64) {
-    if (nrows <= 32) down_tile<BITS, BF16, OUT16, 1, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16);
-    else down_tile<BITS, BF16, OUT16, 2, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16);
+    if (nrows <= 32) down_tile<BITS, BF16, OUT16, 1, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, plane, y32, y16);
+    else down_tile<BITS, BF16, OUT16, 2, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, plane, y32, y16);
   } else {
     switch ((nrows + 31) >> 5) {
-      case 1: down_tile<BITS, BF16, OUT16, 1, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-      case 2: down_tile<BITS, BF16, OUT16, 2, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-      case 3: down_tile<BITS, BF16, OUT16, 3, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
-      default: down_tile<BITS, BF16, OUT16, 4, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, y32, y16); break;
+      case 1: down_tile<BITS, BF16, OUT16, 1, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, plane, y32, y16); break;
+      case 2: down_tile<BITS, BF16, OUT16, 2, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, plane, y32, y16); break;
+      case 3: down_tile<BITS, BF16, OUT16, 3, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, plane, y32, y16); break;
+      default: down_tile<BITS, BF16, OUT16, 4, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, plane, y32, y16); break;
     }
   }
 }
@@ -599,7 +648,7 @@ template <int BITS, bool BF16, int ACT>
 static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, const Work& w, int max_mtiles,
                             uint16_t* y16, const float* wscale, hipStream_t s) {
   const LayerArgs& L = c.args;
-  (void)T;
+  const size_t plane = (size_t)T * c.top_k * L.I;  // act lo plane offset (the workspace holds both planes)
   const int per_xcd = (max_mtiles + 7) / 8;  // m-tiles of one XCD's share at most (see xcd_mtile)
   const dim3 grid_gu(8 * per_xcd * ((L.I + GU_COLS - 1) / GU_COLS));
   // weights from the prefill copy when the layer has one, else the MLX tensors with scales in
@@ -610,7 +659,7 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
   const int bl_dn = pk ? 2 : (L.I / GROUP) % 2 == 0 ? 1 : 0;
 #define KMOE_GU(BLV, BMV)                                                                                    \
   KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, BLV, BMV>), grid_gu, dim3(256), 0, s, L, \
-              x, c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act)
+              x, c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act, plane)
   if (bl_gu == 2) {
     if (bm == 64) KMOE_GU(2, 64); else KMOE_GU(2, 128);
   } else if (bl_gu == 1) KMOE_GU(1, 128); else KMOE_GU(0, 128);
@@ -620,7 +669,7 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
   const dim3 grid_dn(8 * per_xcd * ((L.H + DN_COLS - 1) / DN_COLS));
 #define KMOE_DOWN(OUT16, BLV, BMV)                                                                              \
   KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, OUT16, BLV, BMV>), grid_dn, dim3(256), 0, s, L,   \
-              w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, wscale,             \
+              w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, plane, wscale,      \
               OUT16 ? (float*)nullptr : w.y32, OUT16 ? y16 : (uint16_t*)nullptr)
   if (y16) {
     if (bl_dn == 2) {
@@ -646,6 +695,26 @@ hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Wor
   if (c.bf16_scales)
     return c.act ? gemm_impl<4, true, 1>(c, x, T, w, max_mtiles, y16, wscale, s) : gemm_impl<4, true, 0>(c, x, T, w, max_mtiles, y16, wscale, s);
   return c.act ? gemm_impl<4, false, 1>(c, x, T, w, max_mtiles, y16, wscale, s) : gemm_impl<4, false, 0>(c, x, T, w, max_mtiles, y16, wscale, s);
+}
+
+// y[a] = 0 for the assignments whose expert index lies outside [0, E).  The permutation drops
+// them (and sets DEVERR_BAD_EXPERT), so the grouped GEMMs never write their rows; the decode path
+// writes zeros for them, and this gives the grouped path the same result.  One thread per
+// assignment; only the rare bad rows store anything.
+__global__ __launch_bounds__(256) void zero_bad_rows_kernel(const int32_t* __restrict__ idx, int TK, int E, int H,
+                                                            uint16_t* __restrict__ y) {
+  const int a = blockIdx.x * 256 + threadIdx.x;
+  if (a >= TK) return;
+  const int e = idx[a];
+  if (e >= 0 && e < E) return;
+  uint4* row = reinterpret_cast<uint4*>(y + (size_t)a * H);
+  for (int q = 0; q < H / 8; ++q) row[q] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+hipError_t launch_zero_bad_rows(const int32_t* idx, int TK, int E, int H, uint16_t* y, hipStream_t s) {
+  if (TK == 0) return hipSuccess;
+  KMOE_LAUNCH("zero_bad_rows_kernel", zero_bad_rows_kernel, dim3((TK + 255) / 256), dim3(256), 0, s, idx, TK, E, H, y);
+  return hipGetLastError();
 }
 
 hipError_t launch_xpair(const LayerConfig& c, const uint16_t* x, int T, uint16_t* xpp, hipStream_t s) {

@@ -124,6 +124,8 @@ class QuantizedExperts:
         self._handle = h
         self._ws = None
         self._ws_tokens = -1
+        self._ws_captured = False   # the current workspace was used by a captured call
+        self._ws_retired = []       # earlier workspaces still referenced by captured graphs
 
     # ---- construction helpers ---------------------------------------------------------
     @classmethod
@@ -189,6 +191,31 @@ class QuantizedExperts:
         act = activation or ("gelu_tanh" if hdr.intermediate == 704 else "swiglu")
         return cls(shape, _block_projs(buf, geom, hdr.expert_size), hdr.scale_dtype, act, None, [buf], prefill_copy)
 
+    @classmethod
+    def from_safetensors(cls, path: str, layer: int, top_k: int, device="cuda", prefix: str | None = None,
+                         activation: str = "swiglu", layout: str = "expert",
+                         prefill_copy: bool = False) -> "QuantizedExperts":
+        """Load one MoE layer's stacked ``switch_mlp`` tensors from an MLX safetensors checkpoint
+        (a directory with ``model.safetensors.index.json`` or ``model.safetensors``, or one
+        file); dimensions, bit width and scale dtype come from the tensor shapes
+        (kandiga/_split_experts.py:62-117 reads the same nine tensors)."""
+        from . import weights
+
+        L, info = weights.read_switch_mlp(path, layer, prefix or weights.DEFAULT_PREFIX)
+        shape = LayerShape(info.hidden, info.intermediate, info.num_experts, top_k, info.bits)
+        return cls.from_stacked(shape, L, device, info.scale_dtype, activation, layout, prefill_copy)
+
+    @classmethod
+    def from_expert_files(cls, layer_dir: str, top_k: int, device="cuda", activation: str = "swiglu",
+                          layout: str = "expert", prefill_copy: bool = False) -> "QuantizedExperts":
+        """Load a ``layer_XX/expert_NNN.safetensors`` directory, the per-expert files of the
+        reference's split step (kandiga/_split_experts.py:106-115)."""
+        from . import weights
+
+        L, info = weights.read_expert_files(layer_dir)
+        shape = LayerShape(info.hidden, info.intermediate, info.num_experts, top_k, info.bits)
+        return cls.from_stacked(shape, L, device, info.scale_dtype, activation, layout, prefill_copy)
+
     def with_prefill_copy(self) -> "QuantizedExperts":
         """The same experts (sharing these tensors) with a prefill copy made for them."""
         return QuantizedExperts(self.shape, self.projs, self.scale_dtype, self.activation, self.shared,
@@ -202,13 +229,27 @@ class QuantizedExperts:
         return n.value
 
     def reserve(self, tokens: int) -> None:
-        """Allocate (zeroed) workspace for calls of up to ``tokens`` tokens."""
+        """Allocate (zeroed) workspace for calls of up to ``tokens`` tokens.
+
+        A larger request replaces the workspace.  A workspace that was handed to a call under
+        CUDA-graph capture is never released: the captured graph keeps its address, so it is
+        retained for the life of this object (a later, larger eager call then gets a new one).
+        Growing is refused while a capture is in progress (allocate with ``reserve`` before
+        capturing)."""
         if tokens > self._ws_tokens:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"workspace for {tokens} tokens was not reserved before graph capture "
+                                   f"(reserved: {self._ws_tokens}); call reserve({tokens}) first")
+            if self._ws is not None and self._ws_captured:
+                self._ws_retired.append(self._ws)
             self._ws = torch.zeros(max(self.workspace_bytes(tokens), 256), dtype=torch.uint8, device=self.device)
             self._ws_tokens = tokens
+            self._ws_captured = False
 
     def workspace(self, tokens: int) -> torch.Tensor:
         self.reserve(tokens)
+        if torch.cuda.is_current_stream_capturing():
+            self._ws_captured = True
         return self._ws
 
     def host_subset(self, experts) -> dict:
@@ -258,6 +299,17 @@ class QuantizedExperts:
             self._handle = None
 
 
+def _on_device(t: torch.Tensor, dev: torch.device, name: str) -> None:
+    """Raise before any launch unless ``t`` lives in device memory of ``dev``: a host tensor's
+    pointer handed to a kernel would be a GPU memory fault."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} is on {t.device}; move it to {dev} first")
+    if dev is not None and t.device.index != dev.index:
+        raise ValueError(f"{name} is on {t.device}, the experts are on {dev}")
+
+
 def _check_x(x: torch.Tensor, H: int) -> torch.Tensor:
     if x.shape[-1] != H:
         raise ValueError(f"last dimension of x is {x.shape[-1]}, expected {H}")
@@ -279,6 +331,8 @@ class QuantizedSwitchGLU:
 
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         E = self.experts
+        _on_device(x, E.device, "x")
+        _on_device(indices, E.device, "indices")
         K = indices.shape[-1]
         if K != E.shape.top_k:
             raise ValueError(f"indices have {K} experts per token, layer was built for top_k={E.shape.top_k}")
@@ -311,6 +365,8 @@ class SparseMoeBlock:
         E = self.experts
         if out_dtype not in (torch.float16, torch.float32):
             raise TypeError("out_dtype must be torch.float16 or torch.float32")
+        _on_device(x, E.device, "x")
+        _on_device(logits, E.device, "logits")
         lead = x.shape[:-1]
         xf = _check_x(x, E.shape.hidden)
         lg = logits.reshape(-1, E.shape.num_experts).to(torch.float32).contiguous()
@@ -335,6 +391,7 @@ class SparseMoeBlock:
 
 def route(logits: torch.Tensor, top_k: int):
     """Top-K experts per token (ties -> lower index) and renormalised softmax weights."""
+    _on_device(logits, None, "logits")
     lg = logits.to(torch.float32).contiguous()
     T, E = lg.reshape(-1, lg.shape[-1]).shape
     idx = torch.empty((T, top_k), dtype=torch.int32, device=lg.device)
@@ -347,6 +404,7 @@ def route(logits: torch.Tensor, top_k: int):
 
 def permute(idx: torch.Tensor, num_experts: int) -> dict:
     """Stable token->expert grouping: perm, counts, offsets, unique experts (engine.py:407-418)."""
+    _on_device(idx, None, "idx")
     K = idx.shape[-1]
     ii = idx.reshape(-1, K).to(torch.int32).contiguous()
     T = ii.shape[0]
@@ -374,6 +432,8 @@ def permute(idx: torch.Tensor, num_experts: int) -> dict:
 
 def combine(y: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
     """``out[t] = sum_k w[t,k] * y[t,k]`` (fp32 accumulate, fp16 out) for y ``[..., K, H]`` fp16."""
+    _on_device(y, None, "y")
+    _on_device(weights, y.device, "weights")
     K, H = y.shape[-2], y.shape[-1]
     yy = y.reshape(-1, K, H).to(torch.float16).contiguous()
     ww = weights.reshape(-1, K).to(torch.float32).contiguous()

@@ -9,10 +9,16 @@ Pins (each function's docstring names its checks in ``tests/``):
 
 * ``unpack_codes``      known-answer byte patterns, pack/unpack round trip, the BKEX
                         offset constants of kandiga_cpu_expert.m:42-65.
-* ``dequantize``        closed form ``(q - 2**(b-1)) * s`` exact for the synthetic scales.
-* ``route``             brute force over E on small inputs, softmax identities, tie cases.
+* ``dequantize``        closed form ``(q - 2**(b-1)) * s`` exact for the synthetic scales;
+                        element-by-element brute force (codes read bit by bit) on general,
+                        independent fp16/bf16 scale/bias pairs.
+* ``route``             brute force over E on small inputs, softmax identities, tie cases,
+                        NaN and infinite logits.
 * ``permute``           brute-force ``sorted(range(T*K), key=(expert, flat index))``.
 * ``combine``           closed form ``sum_k w_k y_k``, linearity.
 * ``switch_mlp`` (C)    float64 numpy matmul over fully dequantized matrices
-                        (``expert_mlp_f64``), zero-weight and one-hot special cases.
+                        (``expert_mlp_f64``), zero-weight and one-hot special cases; the
+                        GELU-tanh mode against ``torch.nn.functional.gelu(approximate='tanh')``.
+* ``shared_expert_f64`` closed form for constant matrices (with a gate/up swap that must
+                        differ) and explicit index loops on non-square matrices.
 """

@@ -77,7 +77,8 @@ def dequantize(words, scales, biases, bits: int, in_dim: int, scale_dtype: str =
 def route(logits: np.ndarray, top_k: int):
     """Top-K experts per token with weights renormalised over the selected K.
 
-    Selection key: logit descending, expert index ascending on equal logits.  The
+    Selection key: logit descending, expert index ascending on equal logits; NaN logits
+    rank below every number (-inf included).  The
     reference's router (kandiga/metal/moe_block.metal:419-505; mlx_lm's
     softmax -> argpartition -> renorm on the live path) selects on the softmax
     probabilities with lowest-index ties; softmax is monotone in the logit, so the two
@@ -96,8 +97,9 @@ def route(logits: np.ndarray, top_k: int):
     order = np.argsort(-logits, axis=1, kind="stable")       # ties: lower index first
     idx = order[:, :top_k].astype(np.int32)
     sel = np.take_along_axis(logits, idx, axis=1).astype(np.float64)
-    e = np.exp(sel - sel[:, :1])
-    w = (e / e.sum(axis=1, keepdims=True)).astype(np.float32)
+    with np.errstate(invalid="ignore"):   # NaN or infinite logits give NaN weights
+        e = np.exp(sel - sel[:, :1])
+        w = (e / e.sum(axis=1, keepdims=True)).astype(np.float32)
     return idx, w
 
 
@@ -180,6 +182,69 @@ def shared_expert_f64(layer: dict, x: np.ndarray) -> np.ndarray:
 # --------------------------------------------------------------------------------------
 # Expert MLP: float64 closed form and the C restatement
 # --------------------------------------------------------------------------------------
+def dequantize_dense(words, scales, biases, bits: int, in_dim: int, scale_dtype: str = "f16",
+                     dtype=np.float64) -> np.ndarray:
+    """:func:`dequantize` with broadcast unpacking (whole 3-byte triplets / 4-byte words at
+    once), for the full-size checks.  Equal to :func:`dequantize` in float64; in float32 the
+    result is exact whenever ``q*s + b`` is (always for the synthetic scales)."""
+    words = np.ascontiguousarray(words)
+    lead = words.shape[:-1]
+    rows = int(np.prod(lead)) if lead else 1
+    if bits == 4:
+        q = (words.reshape(rows, in_dim // 8, 1) >> (np.arange(8, dtype=np.uint32) * 4)) & 0xF
+    elif bits == 3:
+        b = words.view(np.uint8).reshape(rows, in_dim // 8, 3).astype(np.uint32)
+        t = (b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16))[..., None]
+        q = (t >> (np.arange(8, dtype=np.uint32) * 3)) & 7
+    else:
+        raise ValueError(bits)
+    q = q.reshape(rows, in_dim // GROUP, GROUP).astype(dtype)
+    sc = scale_to_f64(scales, scale_dtype).reshape(rows, in_dim // GROUP, 1).astype(dtype)
+    bi = scale_to_f64(biases, scale_dtype).reshape(rows, in_dim // GROUP, 1).astype(dtype)
+    return (q * sc + bi).reshape(*lead, in_dim)
+
+
+def moe_out_dense(expert_arrays, x: np.ndarray, idx: np.ndarray, w: np.ndarray, bits: int, hidden: int,
+                  inter: int, scale_dtype: str = "f16", act: str = "silu", dtype=np.float64,
+                  threads: int = 8) -> np.ndarray:
+    """Routed combine ``out[t] = sum_k w[t,k] * expert_{idx[t,k]}(x[t])`` for every token of a
+    full-size batch, through dense matrix products one expert at a time: all the rows routed
+    to an expert go through its dequantized gate/up/down matrices together.
+
+    ``expert_arrays(e)`` returns expert e's nine arrays (``gate_w``, ``gate_s``, ...,
+    ``down_b``, without the expert dimension).  Experts are spread over ``threads`` workers,
+    each with a single-threaded BLAS.  float64 by default; float32 keeps the relative error
+    near 1e-6, three orders below the layer tolerance, at half the time."""
+    from concurrent.futures import ThreadPoolExecutor
+    from threadpoolctl import threadpool_limits
+
+    idx = np.asarray(idx)
+    T, K = idx.shape
+    xs = np.asarray(x, dtype=np.float16).astype(dtype)
+    wts = np.asarray(w, dtype=np.float64)
+    experts = np.unique(idx)
+
+    def one(e):
+        a = expert_arrays(int(e))
+        tok, kk = np.nonzero(idx == e)
+        g = dequantize_dense(a["gate_w"], a["gate_s"], a["gate_b"], bits, hidden, scale_dtype, dtype)
+        u = dequantize_dense(a["up_w"], a["up_s"], a["up_b"], bits, hidden, scale_dtype, dtype)
+        d = dequantize_dense(a["down_w"], a["down_s"], a["down_b"], bits, inter, scale_dtype, dtype)
+        xr = xs[tok]
+        gv, uv = xr @ g.T, xr @ u.T
+        if act == "silu":
+            av = gv / (1 + np.exp(-gv)) * uv
+        else:
+            av = 0.5 * gv * (1 + np.tanh(0.7978845608 * (gv + 0.044715 * gv ** 3))) * uv
+        return tok, (av @ d.T).astype(np.float64) * wts[tok, kk][:, None]
+
+    out = np.zeros((T, hidden), dtype=np.float64)
+    with threadpool_limits(limits=1, user_api="blas"), ThreadPoolExecutor(max(1, threads)) as pool:
+        for tok, contrib in pool.map(one, experts):
+            np.add.at(out, tok, contrib)
+    return out
+
+
 def expert_weights_f64(layer: dict, e: int, bits: int, hidden: int, inter: int, scale_dtype: str = "f16"):
     g = dequantize(layer["gate_w"][e], layer["gate_s"][e], layer["gate_b"][e], bits, hidden, scale_dtype)
     u = dequantize(layer["up_w"][e], layer["up_s"][e], layer["up_b"][e], bits, hidden, scale_dtype)
@@ -219,7 +284,7 @@ _lib = None
 
 def build_lib(force: bool = False) -> str:
     """Compile ``oracle/expert_mlp.c`` with ``oracle/Makefile``."""
-    if force or not os.path.exists(_LIB_PATH):
+    if force or not os.path.exists(_LIB_PATH) or not os.path.exists(os.path.join(_HERE, "_build", "librefscalar.so")):
         subprocess.run(["make", "-B" if force else "-s", "-C", _HERE], check=True,
                        stdout=subprocess.DEVNULL)
     return _LIB_PATH
@@ -269,6 +334,39 @@ def switch_mlp(layer: dict, x: np.ndarray, idx: np.ndarray, bits: int, scale_dty
                                  int(nthreads))
     if rc != 0:
         raise RuntimeError("oracle_switch_mlp failed")
+    return y
+
+
+_rs_lib = None
+
+
+def ref_scalar_switch_mlp(layer: dict, x: np.ndarray, idx: np.ndarray, bits: int, scale_dtype: str = "f16",
+                          nthreads: int = 1) -> np.ndarray:
+    """The CPU baseline (``oracle/ref_scalar.c``): the reference's portable scalar expert MLP at
+    its own optimisation level, K experts of a token on an OpenMP team -> ``[T, K, H]`` fp32."""
+    global _rs_lib
+    if _rs_lib is None:
+        path = os.path.join(_HERE, "_build", "librefscalar.so")
+        if not os.path.exists(path):
+            build_lib()
+        L = ctypes.CDLL(path)
+        L.refscalar_switch_mlp.argtypes = [ctypes.POINTER(_Layer), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+        L.refscalar_switch_mlp.restype = ctypes.c_int
+        _rs_lib = L
+    H = layer["gate_s"].shape[-1] * GROUP
+    I = layer["down_s"].shape[-1] * GROUP
+    x16 = np.ascontiguousarray(np.asarray(x, dtype=np.float16)).view(np.uint16)
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    T, K = idx.shape
+    if idx.size and (idx.min() < 0 or idx.max() >= layer["gate_w"].shape[0]):
+        raise ValueError("expert index out of range")
+    y = np.empty((T, K, H), dtype=np.float32)
+    desc = _Layer(H, I, bits, 1 if scale_dtype == "bf16" else 0, 0,
+                  _proj(layer, "gate"), _proj(layer, "up"), _proj(layer, "down"))
+    if _rs_lib.refscalar_switch_mlp(ctypes.byref(desc), x16.ctypes.data, idx.ctypes.data, T, K, y.ctypes.data,
+                                    int(nthreads)) != 0:
+        raise RuntimeError("refscalar_switch_mlp failed")
     return y
 
 

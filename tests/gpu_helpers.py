@@ -23,15 +23,16 @@ def assert_close(got, ref, max_abs=MAX_ABS, rel_l2=REL_L2, what="", fp16_out=Non
     """max |got-ref| <= max_abs and rel-L2 <= rel_l2.
 
     For fp16 outputs (``got`` of dtype float16, or ``fp16_out=True``) an element may instead
-    be within one fp16 ulp of the fp32 reference: above |out| = 32 that spacing (1/32)
-    exceeds 2e-2 and no fp16 value can be closer.
+    be within half an fp16 ulp of the fp32 reference plus 2e-3: above |out| = 32 the output
+    rounding alone (half of a 1/32 spacing) exceeds 2e-2 even for a correctly rounded result,
+    and the 2e-3 covers fp32 accumulation-order differences before that rounding.
     """
     is16 = (np.asarray(got).dtype == np.float16) if fp16_out is None else fp16_out
     g = np.asarray(got, dtype=np.float64)
     r = np.asarray(ref, dtype=np.float64)
     err = O.compare(g, r)
     diff = np.abs(g - r)
-    allowed = np.maximum(max_abs, f16_ulp(r)) if is16 else np.full_like(r, max_abs)
+    allowed = np.maximum(max_abs, 0.5 * f16_ulp(r) + 2e-3) if is16 else np.full_like(r, max_abs)
     worst = float((diff - allowed).max()) if diff.size else 0.0
     print(f"  {what}: max_abs={err['max_abs']:.3e} rel_l2={err['rel_l2']:.3e} max|ref|="
           f"{float(np.abs(r).max()) if r.size else 0:.1f} fp16_out={is16}", flush=True)
@@ -66,3 +67,23 @@ def remap(idx: np.ndarray):
     """Distinct experts of idx and idx rewritten as positions into that list."""
     uniq, inv = np.unique(idx, return_inverse=True)
     return uniq, inv.reshape(idx.shape).astype(np.int32)
+
+
+def host_layer(layer) -> dict:
+    """Host numpy copy of a layer dict (numpy or device tensors), 32-bit words as uint32 and
+    16-bit patterns as uint16."""
+    out = {}
+    for k, v in layer.items():
+        a = to_np(v) if isinstance(v, torch.Tensor) else np.asarray(v)
+        out[k] = a.view(np.uint32) if k.endswith("_w") else a.view(np.uint16)
+    return out
+
+
+def dense_reference(layer_h: dict, shape, x, idx, w, scale_dtype="f16", dtype=np.float64):
+    """Oracle output of every row of a full-size batch: routed combine through dense per-expert
+    products (oracle.moe_out_dense) plus the shared expert when the layer has one."""
+    out = O.moe_out_dense(lambda e: {k: v[e] for k, v in layer_h.items() if not k.startswith("shared_")},
+                          x, idx, w, shape.bits, shape.hidden, shape.intermediate, scale_dtype, dtype=dtype)
+    if "shared_gate" in layer_h:
+        out = out + O.shared_expert_f64(layer_h, x)
+    return out

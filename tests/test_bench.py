@@ -22,27 +22,29 @@ def test_cpu_baseline_record():
     from kandiga_amd import synth
 
     shape = synth.LayerShape(512, 256, 16, 4, 3)
-    layer = synth.make_layer(shape, 5)
-
-    class HostExperts:  # the one method cpu_baseline uses, over host arrays
-        def host_subset(self, ids):
-            return {k: v[np.asarray(ids)] for k, v in layer.items()}
-
-    r = bench.cpu_baseline(HostExperts(), shape, 1.0)
+    r = bench.cpu_baseline(shape, 0.5, synth.LayerShape(512, 256, 16, 4, 4))
     assert r["kind"] == "port" and r["unit"] == "GB/s" and r["value"] > 0
     assert r["cores"] == min(shape.top_k, os.cpu_count() or 1, 16)
     assert r["single_thread"]["tokens"] >= 1 and r["single_thread"]["us_per_token"] > 0
+    assert r["checker_restatement"]["us_per_token"] > 0
+    assert r["layer_4bit"]["us_per_token"] > 0
     assert abs(r["prefill_T512_s_extrapolated"] - 512 * r["us_per_token"] * 1e-6) < 1e-3
     assert r["host"]["nproc"] == os.cpu_count()
 
 
-def test_stage1_traffic_matches_committed_summary():
+def test_kernel_traffic_reads_committed_summaries():
+    """Every committed counter summary turns into a traffic figure: (FETCH + WRITE) KiB per
+    dispatch over the copy-calibrated ratios; a kernel without a summary gives null."""
+    import glob
+
     import bench
 
-    with open(bench.TRAFFIC_FILE) as f:
-        t = json.load(f)
-    want = t["fetch_kib_per_dispatch"] * 1024 / t["copy_fetch_ratio"] + t["write_kib_per_dispatch"] * 1024 / t["copy_write_ratio"]
-    got = bench.stage1_traffic(7361600)
-    assert got == round(want)
-    # the kernel reads what it should: within 10% of the algorithmic bytes of the workload
-    assert 1.0 <= got / 7361600 < 1.1
+    files = glob.glob(os.path.join(bench.PROFILES, "*_decode_t1_k8_traffic.json"))
+    assert files
+    for fn in files:
+        with open(fn) as f:
+            t = json.load(f)
+        want = t["fetch_kib_per_dispatch"] * 1024 / t["copy_fetch_ratio"] + \
+            t["write_kib_per_dispatch"] * 1024 / t["copy_write_ratio"]
+        assert bench.kernel_traffic(t["kernel"]) == round(want)
+    assert bench.kernel_traffic("no_such_kernel") is None

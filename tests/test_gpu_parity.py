@@ -11,7 +11,7 @@ import torch
 from kandiga_amd import synth
 from kandiga_amd.layout import unpack_codes
 from oracle import moe_oracle as O
-from tests.gpu_helpers import assert_close, to_np, remap, torch_layer_subset
+from tests.gpu_helpers import assert_close, dense_reference, host_layer, to_np, remap, torch_layer_subset
 
 pytestmark = pytest.mark.gpu
 
@@ -45,6 +45,53 @@ def test_dequantize_bitexact(device, name, scale_dtype):
             assert np.array_equal(to_np(w16).view(np.uint16), ref_w.view(np.uint16)), f"{proj} expert {e} weights"
 
 
+def _general_scale_bias(rng, shape, scale_dtype):
+    """Independent random scales and biases of both signs, 2**-13 .. 2**3 in magnitude."""
+    from kandiga_amd import layout
+
+    mag = np.exp2(rng.uniform(-13, 3, size=shape)) * rng.choice([-1.0, 1.0], size=shape)
+    if scale_dtype == "f16":
+        return layout.f16_bits(mag.astype(np.float16))
+    return layout.f32_to_bf16_bits(mag.astype(np.float32))
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("scale_dtype", ["f16", "bf16"])
+def test_dequantize_bitexact_general_scales(device, bits, scale_dtype):
+    """round(q*s + b) to fp16, bit for bit, on scale/bias pairs that are not tied together
+    (b != -2**(bits-1)*s): the rounding of the dequantized weight itself is checked, including
+    results in the fp16 subnormal range."""
+    from kandiga_amd.moe import QuantizedExperts
+
+    shape = synth.LayerShape(256, 192, 3, 2, bits)
+    layer = synth.make_layer(shape, 13 + bits, scale_dtype)
+    rng = np.random.default_rng(17 + bits)
+    for proj in ("gate", "up", "down"):
+        layer[f"{proj}_s"] = _general_scale_bias(rng, layer[f"{proj}_s"].shape, scale_dtype)
+        layer[f"{proj}_b"] = _general_scale_bias(rng, layer[f"{proj}_b"].shape, scale_dtype)
+    # groups whose bias cancels q*s: b = -s gives exact zeros at q = 1; s = 2**-13 with
+    # b = -(2**-10 - 2**-17) gives q = 8 -> 2**-17 and nearby codes in the fp16 subnormal range
+    tiny = _general_scale_bias(rng, (2,), scale_dtype)
+    tiny[0] = np.float16(2.0 ** -13).view(np.uint16) if scale_dtype == "f16" else 0x3900
+    tiny[1] = np.float16(-(2.0 ** -10 - 2.0 ** -17)).view(np.uint16) if scale_dtype == "f16" else 0xBA7E
+    for proj in ("gate", "up", "down"):
+        layer[f"{proj}_b"][0, 0, :2] = layer[f"{proj}_s"][0, 0, :2] ^ 0x8000
+        layer[f"{proj}_s"][0, 1, 0], layer[f"{proj}_b"][0, 1, 0] = tiny
+    ex = QuantizedExperts.from_stacked(shape, layer, device, scale_dtype)
+    n_sub = 0
+    for proj, rows, in_dim in (("gate", shape.intermediate, shape.hidden), ("up", shape.intermediate, shape.hidden),
+                               ("down", shape.hidden, shape.intermediate)):
+        for e in range(shape.num_experts):
+            _codes, w16 = ex.dequantize(proj, e, 0, rows)
+            ref = O.dequantize(layer[f"{proj}_w"][e], layer[f"{proj}_s"][e], layer[f"{proj}_b"][e], bits, in_dim,
+                               scale_dtype).astype(np.float16)
+            got = to_np(w16)
+            bad = np.nonzero(got.view(np.uint16) != ref.view(np.uint16))
+            assert bad[0].size == 0, f"{proj} expert {e}: {bad[0].size} weights differ, first at {bad[0][0]},{bad[1][0]}"
+            n_sub += int(((np.abs(ref) < 2 ** -14) & (ref != 0)).sum())
+    print(f"  subnormal fp16 weights checked: {n_sub}")
+
+
 @pytest.mark.parametrize("E,K,T", [(16, 4, 5), (256, 8, 1), (256, 8, 333), (256, 4, 8), (512, 10, 67),
                                    (64, 1, 3), (1000, 16, 9)])
 def test_route_bitexact(device, E, K, T):
@@ -58,6 +105,12 @@ def test_route_bitexact(device, E, K, T):
         logits[2, :] = 0.25
     logits[0, : min(E, 4)] = -np.inf
     logits[0, min(E, 4):min(E, 8)] = [-0.0, 0.0, -0.0, 0.0][: max(0, min(E, 8) - min(E, 4))]
+    # NaN ranks below every number: some NaNs among normal logits, and a row of NaNs and -inf
+    if T > 3:
+        logits[3, ::5] = np.nan
+    if T > 4:
+        logits[4, :] = np.nan
+        logits[4, E // 2] = -np.inf
     idx, w = route(torch.from_numpy(logits).to(device), K)
     ref_idx, ref_w = O.route(logits, K)
     assert np.array_equal(to_np(idx), ref_idx)
@@ -65,7 +118,8 @@ def test_route_bitexact(device, E, K, T):
 
 
 @pytest.mark.parametrize("T,K,E,zipf", [(1, 8, 256, False), (8, 8, 256, False), (512, 8, 256, True),
-                                        (4096, 8, 256, True), (333, 10, 512, False), (2000, 4, 7, False)])
+                                        (4096, 8, 256, True), (333, 10, 512, False), (2000, 4, 7, False),
+                                        (1500, 16, 1024, True)])
 def test_permute_bitexact(device, T, K, E, zipf):
     from kandiga_amd.moe import permute, route
 
@@ -286,7 +340,7 @@ def test_combine_matches_closed_form(device):
     w = rng.random((37, 6)).astype(np.float32)
     out = combine(torch.from_numpy(y).to(device), torch.from_numpy(w).to(device))
     ref = O.combine(y.astype(np.float32), w)
-    np.testing.assert_allclose(to_np(out).astype(np.float32), ref, rtol=1e-3, atol=1e-3)
+    assert_close(to_np(out), ref, what="combine")
 
 
 # ---- benchmark-sized layers -------------------------------------------------------------
@@ -324,19 +378,22 @@ def test_decode_full_3bit_fast_mode(device, full3):
         assert_close(to_np(out), ref["out"], what=f"h2048 3bit K=4 T={T}")
 
 
-@pytest.mark.parametrize("T,sample", [(512, 48), (4096, 24)])
-def test_prefill_full_3bit_zipf(device, full3, T, sample):
+@pytest.mark.parametrize("T", [512, 2048, 4096])
+def test_prefill_full_3bit_zipf(device, full3, T):
+    """Every row of the 512/2048/4096-token Zipf-routed prefill against the oracle's dense
+    per-expert products (float64), plus sampled rows through the C restatement."""
     from kandiga_amd.moe import SparseMoeBlock
 
     shape, layer, ex = full3
     x, logits = synth.make_inputs(shape, T, 3000 + T, zipf=True)
     out, idx, w = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device),
-                                     return_routing=True)
+                                     return_routing=True, out_dtype=torch.float32)
     ref_idx, ref_w = O.route(logits, shape.top_k)
     assert np.array_equal(to_np(idx), ref_idx)
-    rows = np.random.default_rng(T).choice(T, sample, replace=False)
+    assert_close(to_np(out), dense_reference(layer, shape, x, ref_idx, ref_w), what=f"h2048 3bit prefill T={T} all rows")
+    rows = np.random.default_rng(T).choice(T, 16, replace=False)
     y = O.switch_mlp(layer, x[rows], ref_idx[rows], 3, nthreads=8)
-    assert_close(to_np(out)[rows], O.combine(y, ref_w[rows]), what=f"h2048 3bit prefill T={T}")
+    assert_close(to_np(out)[rows], O.combine(y, ref_w[rows]), what=f"h2048 3bit prefill T={T} C-oracle rows")
 
 
 @pytest.mark.parametrize("bits", [3, 4])
@@ -372,27 +429,47 @@ def test_decode_full_4bit(device):
         assert_close(to_np(out32), ref["out"], what=f"h2048 4bit T={T} fp32 out")
 
 
+@pytest.mark.parametrize("T", [512, 2048])
+def test_prefill_full_4bit_zipf(device, T):
+    """Every row of a Zipf-routed 4-bit prefill (activations reach ~240 and outputs ~125 in
+    magnitude) against the oracle's dense per-expert products, fp32 and fp16 outputs."""
+    from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
+
+    shape = synth.SHAPES["h2048-e256-i512-k8-4bit"]
+    layer = synth.make_layer(shape, 1002)
+    ex = QuantizedExperts.from_stacked(shape, layer, device)
+    x, logits = synth.make_inputs(shape, T, 3000 + T, zipf=True)
+    xd, ld = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
+    idx, w = O.route(logits, 8)
+    ref = dense_reference(layer, shape, x, idx, w)
+    assert_close(to_np(SparseMoeBlock(ex)(xd, ld, out_dtype=torch.float32)), ref, what=f"h2048 4bit prefill T={T}")
+    assert_close(to_np(SparseMoeBlock(ex)(xd, ld)), ref, what=f"h2048 4bit prefill T={T} fp16 out")
+
+
 def test_wide_layer_h4096_e512_k10(device):
-    """H=4096, E=512, I=1024, K=10 generated on the device; oracle on the selected experts of
-    sampled rows, up to the 4096-token prefill (also from the prefill copy, bit for bit)."""
+    """H=4096, E=512, I=1024, K=10 generated on the device; every row against the oracle (dense
+    per-expert products, float32 for the 1 TFLOP of the 4096-token batch: relative error near
+    1e-6), up to the 4096-token prefill (also from the prefill copy, bit for bit)."""
     from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
 
     shape = synth.SHAPES["h4096-e512-i1024-k10-3bit"]
     layer_t = synth.make_layer_torch(shape, 5001, device)
     ex = QuantizedExperts.from_stacked(shape, layer_t, device)
     packed = ex.with_prefill_copy()
+    layer_h = host_layer(layer_t)
     for T, zipf in ((1, False), (8, False), (300, True), (4096, True)):
         x, logits = synth.make_inputs(shape, T, 5100 + T, zipf=zipf)
         xd, ld = torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device)
-        out = SparseMoeBlock(ex)(xd, ld)
+        out = SparseMoeBlock(ex)(xd, ld, out_dtype=torch.float32)
         if T > 8:
-            assert torch.equal(SparseMoeBlock(packed)(xd, ld), out), f"prefill copy T={T}"
+            assert torch.equal(SparseMoeBlock(packed)(xd, ld, out_dtype=torch.float32), out), f"prefill copy T={T}"
         idx, w = O.route(logits, shape.top_k)
-        rows = np.arange(T) if T <= 8 else np.random.default_rng(T).choice(T, 12, replace=False)
-        uniq, pos = remap(idx[rows])
-        sub = torch_layer_subset(layer_t, uniq)
-        y = O.switch_mlp(sub, x[rows], pos, 3, nthreads=8)
-        assert_close(to_np(out)[rows], O.combine(y, w[rows]), what=f"h4096 e512 T={T}")
+        ref = dense_reference(layer_h, shape, x, idx, w, dtype=np.float32 if T > 1000 else np.float64)
+        assert_close(to_np(out), ref, what=f"h4096 e512 T={T} all rows")
+        if T <= 8:
+            uniq, pos = remap(idx)
+            y = O.switch_mlp(torch_layer_subset(layer_t, uniq), x, pos, 3, nthreads=8)
+            assert_close(to_np(out), O.combine(y, w), what=f"h4096 e512 T={T} C oracle")
 
 
 @pytest.mark.parametrize("T", [1, 3, 8, 9, 200])
@@ -417,28 +494,26 @@ def test_forward_with_shared_expert_small(device, T):
 
 
 def test_hidden2560_layer_with_shared_expert(device):
-    """H=2560, E=256, I=1024, K=8, 3-bit + fp16 shared expert I=1024; oracle on sampled tokens."""
+    """H=2560, E=256, I=1024, K=8, 3-bit + fp16 shared expert I=1024: every row against the
+    oracle (dense per-expert products + the shared expert, float64)."""
     from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
 
     shape = synth.SHAPES["h2560-e256-i1024-k8-3bit-shared1024"]
     layer_t = synth.make_layer_torch(shape, 6001, device)
     ex = QuantizedExperts.from_stacked(shape, layer_t, device)
+    layer_h = host_layer(layer_t)
     for T, zipf in ((1, False), (8, False), (2048, True)):
         x, logits = synth.make_inputs(shape, T, 6100 + T, zipf=zipf)
         out = SparseMoeBlock(ex)(torch.from_numpy(x).to(device), torch.from_numpy(logits).to(device),
                                  out_dtype=torch.float32)
         idx, w = O.route(logits, shape.top_k)
-        rows = np.arange(T) if T <= 8 else np.random.default_rng(T).choice(T, 12, replace=False)
-        uniq, pos = remap(idx[rows])
-        sub = torch_layer_subset(layer_t, uniq)
-        y = O.switch_mlp(sub, x[rows], pos, 3, nthreads=8)
-        ref = (O.combine(y, w[rows]).astype(np.float64) + O.shared_expert_f64(sub, x[rows])).astype(np.float32)
-        assert_close(to_np(out)[rows], ref, what=f"h2560 shared T={T}")
+        assert_close(to_np(out), dense_reference(layer_h, shape, x, idx, w), what=f"h2560 shared T={T} all rows")
 
 
 def test_decode_graph_replays_match_eager(device):
-    """Several replays of a captured stack of decode layers, with eager work between them,
-    each bit-identical to the eager result (the fused kernel resets its own counters)."""
+    """Several replays of a captured stack of decode layers, with eager work between them
+    (including a larger call that grows the workspaces), each bit-identical to the eager
+    result."""
     from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock
 
     shape = synth.LayerShape(512, 256, 32, 8, 3)
@@ -462,12 +537,16 @@ def test_decode_graph_replays_match_eager(device):
     with torch.cuda.graph(g):
         for i, (b, a) in enumerate(zip(blocks, ins)):
             outs[i] = b(*a)
+    big = [tuple(torch.from_numpy(a).to(device) for a in synth.make_inputs(shape, 64, 750 + i)) for i in range(3)]
     for rep in range(4):
         g.replay()
         torch.cuda.synchronize()
         for i in range(3):
             assert torch.equal(outs[i], eager[i]), f"replay {rep} layer {i}"
         _ = [b(*a) for b, a in zip(blocks, ins)]   # eager work between replays
+        if rep == 1:
+            # a larger eager call grows the workspace; the captured graph keeps its own
+            _ = [b(*a) for b, a in zip(blocks, big)]
         torch.cuda.synchronize()
     for b in blocks:
         assert b.experts.device_status() == 0

@@ -229,3 +229,143 @@ def test_golden_fixture_reproduces():
         np.testing.assert_allclose(case["w"], data[f"{name}.w"], rtol=1e-6)
         np.testing.assert_allclose(case["y"], data[f"{name}.y"], rtol=1e-5, atol=1e-6)
         np.testing.assert_allclose(case["out"], data[f"{name}.out"], rtol=1e-5, atol=1e-6)
+
+
+# ---- router: NaN and infinities ------------------------------------------------------------
+def test_route_nan_and_inf_ordering():
+    """NaN logits rank below every number (-inf included), ties among them to the lower index;
+    brute force with an explicit (class, value, index) key."""
+    rng = np.random.default_rng(8)
+    logits = rng.standard_normal((6, 40)).astype(np.float32)
+    logits[0, [3, 7, 11]] = np.nan
+    logits[1, :] = np.nan
+    logits[1, [5, 9]] = -np.inf
+    logits[2, ::2] = -np.inf
+    logits[3, [0, 1]] = np.inf
+    logits[4, :38] = np.nan
+    idx, w = O.route(logits, 8)
+
+    def key(v, e):
+        return (1, 0.0, e) if np.isnan(v) else (0, -float(v), e)
+
+    for t in range(logits.shape[0]):
+        brute = sorted(range(40), key=lambda e: key(logits[t, e], e))[:8]
+        assert list(idx[t]) == brute, t
+    assert list(idx[1][:2]) == [5, 9] and list(idx[1][2:]) == [0, 1, 2, 3, 4, 6]
+    assert np.isnan(w[1]).all() and np.isnan(w[4]).all()   # a selected NaN makes the renorm NaN
+    assert not np.isnan(w[0]).any() and not np.isnan(w[2]).any()
+
+
+# ---- dequantization with general scale/bias pairs ------------------------------------------
+def _general_scale_bias(rng, shape, scale_dtype):
+    """Independent random scales and biases (not b = -2**(bits-1)*s), both signs, spanning
+    2**-13 .. 2**3 in magnitude, as 16-bit patterns of ``scale_dtype``."""
+    mag = np.exp2(rng.uniform(-13, 3, size=shape)) * rng.choice([-1.0, 1.0], size=shape)
+    if scale_dtype == "f16":
+        return layout.f16_bits(mag.astype(np.float16))
+    return layout.f32_to_bf16_bits(mag.astype(np.float32))
+
+
+@pytest.mark.parametrize("bits,scale_dtype", [(3, "f16"), (4, "f16"), (3, "bf16"), (4, "bf16")])
+def test_dequantize_brute_force_general_scales(bits, scale_dtype):
+    """Element by element: code of column c read from the packed bytes bit by bit (LSB-first
+    bit stream), w = q * s[c // 64] + b[c // 64] with Python floats."""
+    rng = np.random.default_rng(bits * 10 + len(scale_dtype))
+    rows, cols = 3, 192
+    codes = rng.integers(0, 2 ** bits, size=(rows, cols))
+    words = layout.pack_codes(codes, bits)
+    s = _general_scale_bias(rng, (rows, cols // 64), scale_dtype)
+    b = _general_scale_bias(rng, (rows, cols // 64), scale_dtype)
+    got = O.dequantize(words, s, b, bits, cols, scale_dtype)
+    raw = words.view(np.uint8).reshape(rows, -1)
+
+    def f(u):
+        if scale_dtype == "f16":
+            return float(np.uint16(u).view(np.float16))
+        return float(np.uint32(int(u) << 16).view(np.float32))
+
+    for r in range(rows):
+        for c in range(cols):
+            q = sum(((int(raw[r, (c * bits + i) // 8]) >> ((c * bits + i) % 8)) & 1) << i for i in range(bits))
+            assert q == codes[r, c]
+            assert got[r, c] == q * f(s[r, c // 64]) + f(b[r, c // 64]), (r, c)
+
+
+# ---- dense shared expert ------------------------------------------------------------------
+def test_shared_expert_closed_form_constant_weights():
+    """Constant gate/up/down matrices a, b, c: every intermediate unit is silu(a*S)*(b*S) with
+    S = sum(x), and every output is c * Is * that.  A gate/up swap gives a different value."""
+    H, Is = 128, 64
+    a, b, c = 0.0625, -0.03125, 0.015625
+    layer = {"shared_gate": layout.f16_bits(np.full((Is, H), a, np.float16)),
+             "shared_up": layout.f16_bits(np.full((Is, H), b, np.float16)),
+             "shared_down": layout.f16_bits(np.full((H, Is), c, np.float16))}
+    x = (np.linspace(-1, 2, 3 * H).reshape(3, H)).astype(np.float16)
+    S = x.astype(np.float64).sum(axis=1, keepdims=True)
+    g, u = a * S, b * S
+    want = np.repeat(c * Is * (g / (1 + np.exp(-g))) * u, H, axis=1)
+    got = O.shared_expert_f64(layer, x)
+    np.testing.assert_allclose(got, want, rtol=1e-12)
+    swapped = c * Is * (u / (1 + np.exp(-u))) * g
+    assert (np.abs(swapped - want[:, :1]) > 1e-2 * np.abs(want[:, :1])).all()
+
+
+def test_shared_expert_brute_force_loops():
+    """Random non-square matrices (H != Is) against explicit index loops: out[t, h] =
+    sum_i down[h, i] * silu(sum_j gate[i, j] x[t, j]) * sum_j up[i, j] x[t, j]."""
+    rng = np.random.default_rng(21)
+    H, Is, T = 24, 16, 3
+    gate = (rng.standard_normal((Is, H)) * 0.3).astype(np.float16)
+    up = (rng.standard_normal((Is, H)) * 0.3).astype(np.float16)
+    down = (rng.standard_normal((H, Is)) * 0.3).astype(np.float16)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    layer = {"shared_gate": layout.f16_bits(gate), "shared_up": layout.f16_bits(up),
+             "shared_down": layout.f16_bits(down)}
+    got = O.shared_expert_f64(layer, x)
+    for t in range(T):
+        for h in range(H):
+            acc = 0.0
+            for i in range(Is):
+                gi = sum(float(gate[i, j]) * float(x[t, j]) for j in range(H))
+                ui = sum(float(up[i, j]) * float(x[t, j]) for j in range(H))
+                acc += float(down[h, i]) * (gi / (1 + np.exp(-gi))) * ui
+            assert abs(got[t, h] - acc) <= 1e-12 * max(1.0, abs(acc)), (t, h)
+
+
+# ---- GELU-tanh gate of the C restatement ----------------------------------------------------
+def test_switch_mlp_gelu_tanh_matches_torch_gelu():
+    """act == 1 (kandiga_cpu_expert_lg.m:237-245) against an f64 reference whose gate activation
+    is torch.nn.functional.gelu(approximate='tanh') on the CPU; SwiGLU must differ."""
+    import torch
+
+    shape = synth.LayerShape(192, 128, 5, 2, 3)
+    for scale_dtype in ("f16", "bf16"):
+        layer = synth.make_layer(shape, 23, scale_dtype)
+        x, logits = synth.make_inputs(shape, 3, 24)
+        idx, _ = O.route(logits, 2)
+        y = O.switch_mlp(layer, x, idx, 3, scale_dtype, act="gelu", nthreads=2)
+        y_silu = O.switch_mlp(layer, x, idx, 3, scale_dtype, act="silu")
+        for t in range(3):
+            for k in range(2):
+                g_w, u_w, d_w = O.expert_weights_f64(layer, idx[t, k], 3, 192, 128, scale_dtype)
+                xs = x[t].astype(np.float64)
+                g = torch.from_numpy(g_w @ xs)
+                a = torch.nn.functional.gelu(g, approximate="tanh").numpy() * (u_w @ xs)
+                ref = d_w @ a
+                assert O.compare(y[t, k], ref)["rel_l2"] < 2e-6, (scale_dtype, t, k)
+                assert O.compare(y_silu[t, k], ref)["rel_l2"] > 1e-2
+
+
+# ---- CPU baseline ---------------------------------------------------------------------------
+@pytest.mark.parametrize("bits,scale_dtype", [(3, "bf16"), (4, "bf16"), (3, "f16")])
+def test_ref_scalar_baseline_computes_the_same_layer(bits, scale_dtype):
+    """The CPU baseline (the reference's scalar loops, one accumulator, default contraction)
+    agrees with the checker to fp32 accumulation-order accuracy, single- and multi-threaded."""
+    shape = synth.LayerShape(256, 128, 8, 4, bits)
+    layer = synth.make_layer(shape, 27, scale_dtype)
+    x, logits = synth.make_inputs(shape, 3, 28)
+    idx, _ = O.route(logits, 4)
+    ref = O.switch_mlp(layer, x, idx, bits, scale_dtype)
+    for nt in (1, 4):
+        got = O.ref_scalar_switch_mlp(layer, x, idx, bits, scale_dtype, nthreads=nt)
+        assert O.compare(got, ref)["rel_l2"] < 1e-5
