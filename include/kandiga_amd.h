@@ -157,6 +157,20 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
                  void* stream);
 
 /*
+ * kmoe_forward without a workspace argument: the library's own static device scratch of
+ * KMOE_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends) serves as the workspace, and
+ * the call allocates nothing (no hipMalloc, no allocating library routine).  No counterpart in
+ * the reference; for callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  Calls whose kmoe_workspace_size exceeds
+ * the scratch fail with KMOE_ERR_WORKSPACE before anything is launched (every decode batch fits;
+ * prefill up to about T*K*H*4 + T*K*I*4 bytes).  All calls on one GPU share its scratch: calls
+ * that overlap on one GPU race.  Device error flags are not readable through this entry point.
+ */
+#define KMOE_NOALLOC_SCRATCH_BYTES (16u << 20)
+int kmoe_forward_noalloc(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
+                         int32_t out_dtype, int32_t* idx_out, float* weights_out, void* stream);
+
+/*
  * Prefill weight copy.  No counterpart in the reference, whose routed experts exist only in
  * the MLX layout; for callers that run prefill and can hold a second copy of the experts (about
  * the size of the codes plus scales).  kmoe_prefill_pack rewrites every expert of `desc` into a

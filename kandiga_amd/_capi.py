@@ -18,7 +18,7 @@ EXPORTS = (
     "kmoe_version", "kmoe_strerror", "kmoe_last_error",
     "kmoe_layer_create", "kmoe_layer_destroy", "kmoe_workspace_size",
     "kmoe_route", "kmoe_permute_workspace_size", "kmoe_permute",
-    "kmoe_expert_mlp", "kmoe_combine", "kmoe_forward",
+    "kmoe_expert_mlp", "kmoe_combine", "kmoe_forward", "kmoe_forward_noalloc",
     "kmoe_prefill_pack_size", "kmoe_prefill_pack",
     "kmoe_dequantize", "kmoe_device_status",
     "kmoe_profile_begin", "kmoe_profile_end",
@@ -31,6 +31,7 @@ SCALE_F16, SCALE_BF16 = 0, 1
 ACT_SWIGLU, ACT_GELU_TANH = 0, 1
 OUT_F16, OUT_F32 = 0, 1
 DEVERR_BAD_EXPERT = 1
+NOALLOC_SCRATCH_BYTES = 16 << 20
 DEVERR_SPIN = 2
 
 
@@ -81,6 +82,7 @@ def _declare(L):
         "kmoe_expert_mlp": ([_vp, _vp, _vp, _i32, _vp, _vp, _sz, _vp], ctypes.c_int),
         "kmoe_combine": ([_vp, _vp, _i32, _i32, _i32, _vp, _vp], ctypes.c_int),
         "kmoe_forward": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
+        "kmoe_forward_noalloc": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp], ctypes.c_int),
         "kmoe_prefill_pack_size": ([P(LayerDesc), P(_sz)], ctypes.c_int),
         "kmoe_prefill_pack": ([P(LayerDesc), _vp, _sz, _vp], ctypes.c_int),
         "kmoe_dequantize": ([_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp], ctypes.c_int),

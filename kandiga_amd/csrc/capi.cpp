@@ -377,6 +377,17 @@ int kmoe_combine(const void* y, const float* weights, int32_t tokens, int32_t to
 int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                  int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
                  void* stream) {
+  return kmoe::forward_impl(layer, x, logits, tokens, out, out_dtype, idx_out, weights_out, workspace,
+                            workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+// The routed layer on a caller-provided workspace (kmoe_forward, and kmoe_forward_noalloc with the
+// library's static scratch).
+int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
+                       int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace,
+                       size_t workspace_bytes, void* stream) {
   if (!layer) return fail(KMOE_ERR_INVALID_ARG, "null layer");
   if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
   if (out_dtype != KMOE_OUT_F16 && out_dtype != KMOE_OUT_F32) return fail(KMOE_ERR_INVALID_ARG, "unknown out_dtype");
@@ -414,6 +425,14 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
   }
   return e == hipSuccess ? ok() : hip_fail(e, "forward launch");
 }
+
+int kmoe::workspace_bytes_for(const kmoe_layer* layer, int32_t tokens, size_t* bytes) {
+  return kmoe_workspace_size(layer, tokens, bytes);
+}
+
+int kmoe::report_error(int code, const char* msg) { return fail(code, "%s", msg); }
+
+extern "C" {
 
 int kmoe_dequantize(const kmoe_layer* layer, int32_t proj, int32_t expert, int32_t row0, int32_t nrows,
                     uint8_t* codes, uint16_t* weights_f16, void* stream) {

@@ -116,6 +116,22 @@ void prof_events(const char* kernel_name, hipStream_t s, hipEvent_t* start, hipE
       hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, __VA_ARGS__);                         \
   } while (0)
 
+}  // namespace kmoe
+
+struct kmoe_layer;
+
+namespace kmoe {
+
+// The routed layer (kmoe_forward's body) on the given workspace; the status and last error are
+// those of kmoe_forward.
+int forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
+                 int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
+                 void* stream);
+// kmoe_workspace_size for `tokens` tokens of `layer`.
+int workspace_bytes_for(const kmoe_layer* layer, int32_t tokens, size_t* bytes);
+// Records `msg` as the calling thread's last error and returns `code`.
+int report_error(int code, const char* msg);
+
 // ---- launchers (return hipError_t of the launch) ----------------------------------------
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s);
 // launch_route plus xpp = x [T][H] in pair order for `bits`-bit codes (one launch).
