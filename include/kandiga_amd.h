@@ -157,6 +157,49 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
                  void* stream);
 
 /*
+ * The whole MoE block mlp(x) of the decoder layer: router projection over the quantized
+ * mlp.gate (fp32 logits), softmax -> top-K -> renorm, the routed experts, the quantized shared
+ * expert mlp.shared_expert gated by sigmoid(mlp.shared_expert_gate . x), and an optional
+ * residual:  out = (residual + sum_k w_k y_k) + fp16(shared(x)) * sigmoid(gate . x).
+ * Replaces mlx_lm's Qwen MoE block as driven by kandiga/engine.py:1090-1139, restated in
+ * kandiga/metal/moe_block.metal:194-227 (router_matmul_kernel), :240-336 (shared expert and its
+ * gate), :419-505 (router_softmax_topk), :515-584 (blend_kernel / blend_residual_kernel), the
+ * MoE step of kandiga/metal/full_forward_lg.m:1316-1350, 1635-1735 (bakan_forward_moe_block,
+ * kandiga/metal/bakan_forward.h:111-140).
+ * The router, shared expert and shared gate share one bit width (3 or 4, group 64) and scale
+ * dtype, which may differ from the routed experts' (a 3-bit routed stack beside 4-bit
+ * projections).  The routed layer must not carry a dense shared expert.
+ */
+typedef struct {
+  const kmoe_layer* routed;        /* the routed experts (kmoe_layer_create); must outlive the block */
+  kmoe_qproj router;               /* mlp.gate: [num_experts][hidden]; expert strides ignored */
+  kmoe_qproj shared_gate_proj;     /* mlp.shared_expert.gate_proj [Is][hidden]; weight NULL: no shared expert */
+  kmoe_qproj shared_up_proj;       /* mlp.shared_expert.up_proj [Is][hidden] */
+  kmoe_qproj shared_down_proj;     /* mlp.shared_expert.down_proj [hidden][Is] */
+  kmoe_qproj shared_expert_gate;   /* mlp.shared_expert_gate [1][hidden]; weight NULL: ungated shared expert */
+  int32_t bits;                    /* codes of the four projections above: 3 or 4 */
+  int32_t scale_dtype;             /* KMOE_SCALE_F16 or KMOE_SCALE_BF16 */
+  int32_t shared_intermediate;     /* Is, multiple of 64 */
+  int32_t reserved;
+} kmoe_block_desc;
+
+typedef struct kmoe_block kmoe_block;
+
+int kmoe_block_create(const kmoe_block_desc* desc, kmoe_block** out);
+int kmoe_block_destroy(kmoe_block* block);
+/* Workspace bytes for block calls of up to max_tokens tokens (zero it once after allocating). */
+int kmoe_block_workspace_size(const kmoe_block* block, int32_t max_tokens, size_t* bytes);
+/*
+ *   x device fp16 [tokens][hidden] (the post-attention-norm input of mlp); residual device fp16
+ *   [tokens][hidden] or NULL; out device [tokens][hidden] fp16 or fp32 (out_dtype);
+ *   idx_out / weights_out / logits_out (device, optional) receive the routing and the fp32 router
+ *   logits [tokens][num_experts].
+ */
+int kmoe_block_forward(const kmoe_block* block, const void* x, const void* residual, int32_t tokens, void* out,
+                       int32_t out_dtype, int32_t* idx_out, float* weights_out, float* logits_out, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/*
  * kmoe_forward without a workspace argument: the library's own static device scratch of
  * KMOE_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends) serves as the workspace, and
  * the call allocates nothing (no hipMalloc, no allocating library routine).  No counterpart in

@@ -18,7 +18,9 @@ EXPORTS = (
     "kmoe_version", "kmoe_strerror", "kmoe_last_error",
     "kmoe_layer_create", "kmoe_layer_destroy", "kmoe_workspace_size",
     "kmoe_route", "kmoe_permute_workspace_size", "kmoe_permute",
-    "kmoe_expert_mlp", "kmoe_combine", "kmoe_forward", "kmoe_forward_noalloc",
+    "kmoe_expert_mlp", "kmoe_combine", "kmoe_forward",
+    "kmoe_block_create", "kmoe_block_destroy", "kmoe_block_workspace_size", "kmoe_block_forward",
+    "kmoe_forward_noalloc",
     "kmoe_prefill_pack_size", "kmoe_prefill_pack",
     "kmoe_dequantize", "kmoe_device_status",
     "kmoe_profile_begin", "kmoe_profile_end",
@@ -58,6 +60,13 @@ class LayerDesc(ctypes.Structure):
                 ("prefill_pack", ctypes.c_void_p), ("prefill_pack_bytes", ctypes.c_int64)]
 
 
+class BlockDesc(ctypes.Structure):
+    _fields_ = [("routed", ctypes.c_void_p), ("router", QProjDesc), ("shared_gate_proj", QProjDesc),
+                ("shared_up_proj", QProjDesc), ("shared_down_proj", QProjDesc), ("shared_expert_gate", QProjDesc),
+                ("bits", ctypes.c_int32), ("scale_dtype", ctypes.c_int32), ("shared_intermediate", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
 class KernelTime(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 48), ("launches", ctypes.c_int32), ("reserved", ctypes.c_int32),
                 ("total_ms", ctypes.c_double), ("min_ms", ctypes.c_double), ("max_ms", ctypes.c_double)]
@@ -82,6 +91,10 @@ def _declare(L):
         "kmoe_expert_mlp": ([_vp, _vp, _vp, _i32, _vp, _vp, _sz, _vp], ctypes.c_int),
         "kmoe_combine": ([_vp, _vp, _i32, _i32, _i32, _vp, _vp], ctypes.c_int),
         "kmoe_forward": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
+        "kmoe_block_create": ([P(BlockDesc), P(_vp)], ctypes.c_int),
+        "kmoe_block_destroy": ([_vp], ctypes.c_int),
+        "kmoe_block_workspace_size": ([_vp, _i32, P(_sz)], ctypes.c_int),
+        "kmoe_block_forward": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
         "kmoe_forward_noalloc": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp], ctypes.c_int),
         "kmoe_prefill_pack_size": ([P(LayerDesc), P(_sz)], ctypes.c_int),
         "kmoe_prefill_pack": ([P(LayerDesc), _vp, _sz, _vp], ctypes.c_int),

@@ -349,7 +349,7 @@ int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, 
   uint16_t* yy = static_cast<uint16_t*>(y);
   hipError_t e;
   if (is_decode(tokens, K, c.args.H)) {
-    DecodeCall d{xx, nullptr, idx, tokens, nullptr, nullptr, nullptr, &w, yy, 0, false};
+    DecodeCall d{xx, nullptr, idx, tokens, nullptr, nullptr, nullptr, &w, yy, 0, false, nullptr};
     e = launch_decode(c, d, s);
   } else {
     const int bm = gemm_bm(c.args), mmt = max_mtiles_for(tokens * K, c.args.E, bm);
@@ -387,7 +387,7 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
 // library's static scratch).
 int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                        int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace,
-                       size_t workspace_bytes, void* stream) {
+                       size_t workspace_bytes, void* stream, const float* extra) {
   if (!layer) return fail(KMOE_ERR_INVALID_ARG, "null layer");
   if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
   if (out_dtype != KMOE_OUT_F16 && out_dtype != KMOE_OUT_F32) return fail(KMOE_ERR_INVALID_ARG, "unknown out_dtype");
@@ -412,7 +412,7 @@ int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logi
   if (a.sh_gate) e = launch_shared(c, xx, tokens, w, s);
   if (e != hipSuccess) return hip_fail(e, "shared expert launch");
   if (is_decode(tokens, K, a.H)) {
-    DecodeCall d{xx, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true};
+    DecodeCall d{xx, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true, extra};
     e = launch_decode(c, d, s);
   } else {
     const int bm = gemm_bm(a), mmt = max_mtiles_for(tokens * K, a.E, bm);
@@ -420,8 +420,8 @@ int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logi
     if (e == hipSuccess) e = launch_permute(w.idx, tokens * K, K, a.E, w, mmt, bm, s);
     if (e == hipSuccess) e = launch_gemm(c, w.xpp, tokens, w, mmt, nullptr, w.wts, s);
     if (e == hipSuccess)
-      e = launch_combine(w.y32, nullptr, nullptr, tokens, K, a.H, a.sh_gate ? w.shared_out : nullptr, out, out32,
-                         s);
+      e = launch_combine(w.y32, nullptr, nullptr, tokens, K, a.H, extra ? extra : a.sh_gate ? w.shared_out : nullptr,
+                         out, out32, s);
   }
   return e == hipSuccess ? ok() : hip_fail(e, "forward launch");
 }
@@ -512,6 +512,174 @@ int kmoe_profile_end(kmoe_kernel_time* entries, int32_t max_entries, int32_t* n_
   *n_entries = (int32_t)agg.size();
   for (int32_t i = 0; i < (int32_t)agg.size() && i < max_entries; ++i) entries[i] = agg[i];
   return ok();
+}
+
+}  // extern "C"
+
+// ---- the MoE block around the routed experts ------------------------------------------------
+struct kmoe_block {
+  const kmoe_layer* routed;
+  LayerConfig shared;  // one-expert layer of the quantized shared expert (when has_shared)
+  QProj router, sgate;
+  int bits, bf16, has_shared, gated;
+};
+
+namespace {
+
+struct BlockWork {
+  char* routed;
+  size_t routed_bytes;
+  Work sh;           // the shared layer's carve
+  float* logits;     // [T][E]
+  float* gate;       // [T]
+  int32_t* idx0;     // [T] zeros
+  uint16_t* ysh;     // [T][H] fp16 shared-expert output
+  float* extra;      // [T][H] residual + gated shared term
+};
+
+// Carve a block workspace for T tokens (base == nullptr: size only).
+BlockWork block_carve(const kmoe_block* b, char* base, int T, size_t* total) {
+  BlockWork w{};
+  const LayerArgs& ra = b->routed->cfg.args;
+  size_t routed = 0;
+  kmoe_workspace_size(b->routed, T, &routed);
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> char* {
+    char* p = base ? base + off : nullptr;
+    off += up256(bytes);
+    return p;
+  };
+  w.routed = take(routed);
+  w.routed_bytes = routed;
+  if (b->has_shared) {
+    const LayerArgs& sa = b->shared.args;
+    size_t s1 = 0, s2 = 0;
+    carve(nullptr, T, 1, 1, sa.H, sa.I, 0, false, &s1);
+    carve(nullptr, T, 1, 1, sa.H, sa.I, 0, true, &s2);
+    char* shb = take(s1 > s2 ? s1 : s2);
+    size_t dummy = 0;
+    w.sh = carve(shb, T, 1, 1, sa.H, sa.I, 0, !is_decode(T, 1, sa.H), &dummy);
+  }
+  w.logits = reinterpret_cast<float*>(take((size_t)T * ra.E * 4));
+  w.gate = reinterpret_cast<float*>(take((size_t)T * 4));
+  w.idx0 = reinterpret_cast<int32_t*>(take((size_t)T * 4));
+  w.ysh = reinterpret_cast<uint16_t*>(take((size_t)T * ra.H * 2));
+  w.extra = reinterpret_cast<float*>(take((size_t)T * ra.H * 4));
+  *total = off;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kmoe_block_create(const kmoe_block_desc* d, kmoe_block** out) {
+  if (!d || !out || !d->routed) return fail(KMOE_ERR_INVALID_ARG, "null descriptor, output pointer or routed layer");
+  *out = nullptr;
+  const LayerArgs& ra = d->routed->cfg.args;
+  if (ra.sh_gate) return fail(KMOE_ERR_INVALID_ARG, "the routed layer of a block must not carry a dense shared expert");
+  if (d->bits != 3 && d->bits != 4) return fail(KMOE_ERR_UNSUPPORTED, "block bits must be 3 or 4 (got %d)", d->bits);
+  if (d->scale_dtype != KMOE_SCALE_F16 && d->scale_dtype != KMOE_SCALE_BF16)
+    return fail(KMOE_ERR_INVALID_ARG, "unknown scale_dtype %d", d->scale_dtype);
+  int rc;
+  kmoe_qproj r = d->router;
+  r.weight_expert_stride = r.scale_expert_stride = 0;
+  if ((rc = check_qproj(r, "router", ra.E, ra.H, d->bits, 1))) return rc;
+  kmoe_block tmp{};
+  tmp.routed = d->routed;
+  tmp.bits = d->bits;
+  tmp.bf16 = d->scale_dtype == KMOE_SCALE_BF16;
+  auto qp = [](const kmoe_qproj& q) {
+    return QProj{static_cast<const uint8_t*>(q.weight), static_cast<const uint16_t*>(q.scales),
+                 static_cast<const uint16_t*>(q.biases), 0, 0};
+  };
+  tmp.router = qp(r);
+  tmp.gated = d->shared_expert_gate.weight != nullptr;
+  if (tmp.gated) {
+    kmoe_qproj g = d->shared_expert_gate;
+    g.weight_expert_stride = g.scale_expert_stride = 0;
+    if ((rc = check_qproj(g, "shared_expert_gate", 1, ra.H, d->bits, 1))) return rc;
+    tmp.sgate = qp(g);
+  }
+  tmp.has_shared = d->shared_gate_proj.weight != nullptr;
+  if (tmp.has_shared) {
+    kmoe_layer_desc sd{};
+    sd.hidden = ra.H;
+    sd.intermediate = d->shared_intermediate;
+    sd.num_experts = 1;
+    sd.top_k = 1;
+    sd.bits = d->bits;
+    sd.group_size = 64;
+    sd.scale_dtype = d->scale_dtype;
+    sd.activation = KMOE_ACT_SWIGLU;
+    sd.gate = d->shared_gate_proj;
+    sd.up = d->shared_up_proj;
+    sd.down = d->shared_down_proj;
+    if ((rc = config_from_desc(&sd, &tmp.shared))) return rc;
+  } else if (tmp.gated) {
+    return fail(KMOE_ERR_INVALID_ARG, "a shared expert gate needs a shared expert");
+  }
+  kmoe_block* b = new (std::nothrow) kmoe_block(tmp);
+  if (!b) return fail(KMOE_ERR_NO_MEMORY, "out of host memory");
+  *out = b;
+  return ok();
+}
+
+int kmoe_block_destroy(kmoe_block* block) {
+  delete block;
+  return ok();
+}
+
+int kmoe_block_workspace_size(const kmoe_block* block, int32_t max_tokens, size_t* bytes) {
+  if (!block || !bytes) return fail(KMOE_ERR_INVALID_ARG, "null block or output pointer");
+  if (max_tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "max_tokens must be >= 0");
+  size_t a = 0, b = 0;
+  block_carve(block, nullptr, max_tokens, &a);
+  block_carve(block, nullptr, max_tokens < DEC_MAX_TOKENS ? max_tokens : DEC_MAX_TOKENS, &b);
+  *bytes = a > b ? a : b;
+  return ok();
+}
+
+int kmoe_block_forward(const kmoe_block* block, const void* x, const void* residual, int32_t tokens, void* out,
+                       int32_t out_dtype, int32_t* idx_out, float* weights_out, float* logits_out, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (!block) return fail(KMOE_ERR_INVALID_ARG, "null block");
+  if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
+  if (out_dtype != KMOE_OUT_F16 && out_dtype != KMOE_OUT_F32) return fail(KMOE_ERR_INVALID_ARG, "unknown out_dtype");
+  if (tokens == 0) return ok();
+  if (!x || !out || !workspace) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
+  if (!aligned(x, 16) || !aligned(out, 16) || (residual && !aligned(residual, 16)))
+    return fail(KMOE_ERR_ALIGNMENT, "x, residual and out must be 16-byte aligned");
+  if (logits_out && !aligned(logits_out, 4)) return fail(KMOE_ERR_ALIGNMENT, "logits_out must be 4-byte aligned");
+  size_t need = 0;
+  BlockWork w = block_carve(block, static_cast<char*>(workspace), tokens, &need);
+  if (workspace_bytes < need) return fail(KMOE_ERR_WORKSPACE, "workspace has %zu bytes, needs %zu", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const LayerArgs& ra = block->routed->cfg.args;
+  const uint16_t* xx = static_cast<const uint16_t*>(x);
+  float* logits = logits_out ? logits_out : w.logits;
+  hipError_t e = launch_qlinear(block->router, ra.E, block->sgate, block->gated ? 1 : 0, block->bits, block->bf16, xx,
+                                tokens, ra.H, logits, w.gate, s);
+  if (e == hipSuccess && block->has_shared) {
+    e = launch_fill_i32(w.idx0, tokens, 0, s);
+    const LayerConfig& sc = block->shared;
+    if (e == hipSuccess && is_decode(tokens, 1, ra.H)) {
+      DecodeCall d{xx, nullptr, w.idx0, tokens, nullptr, nullptr, nullptr, &w.sh, w.ysh, 0, false, nullptr};
+      e = launch_decode(sc, d, s);
+    } else if (e == hipSuccess) {
+      const int bm = gemm_bm(sc.args), mmt = max_mtiles_for(tokens, 1, bm);
+      e = launch_permute(w.idx0, tokens, 1, 1, w.sh, mmt, bm, s);
+      if (e == hipSuccess) e = launch_xpair(sc, xx, tokens, w.sh.xpp, s);
+      if (e == hipSuccess) e = launch_gemm(sc, w.sh.xpp, tokens, w.sh, mmt, w.ysh, nullptr, s);
+    }
+  }
+  const bool need_extra = block->has_shared || residual;
+  if (e == hipSuccess && need_extra)
+    e = launch_blend_prep(block->has_shared ? w.ysh : nullptr, block->gated ? w.gate : nullptr,
+                          static_cast<const uint16_t*>(residual), tokens, ra.H, w.extra, s);
+  if (e != hipSuccess) return hip_fail(e, "block launch");
+  return kmoe::forward_impl(block->routed, x, logits, tokens, out, out_dtype, idx_out, weights_out, w.routed,
+                            w.routed_bytes, stream, need_extra ? w.extra : nullptr);
 }
 
 }  // extern "C"

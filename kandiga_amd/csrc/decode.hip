@@ -663,7 +663,7 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   // 8 assignments per workgroup.  Below 32 assignments short row blocks over all tokens are
   // faster.
   const int32_t* idx = d.idx_in ? d.idx_in : d.idx_out;
-  const float* sho = L.sh_gate ? (const float*)w.shared_out : (const float*)nullptr;
+  const float* sho = d.extra ? d.extra : L.sh_gate ? (const float*)w.shared_out : (const float*)nullptr;
   auto stage2 = [&](auto srows, auto rpw, int TG) {
     constexpr int SR = decltype(srows)::value, RP = decltype(rpw)::value, UF = 2;
     const dim3 grid2(L.H / SR, (T + TG - 1) / TG);

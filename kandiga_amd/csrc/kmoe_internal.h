@@ -98,6 +98,8 @@ struct DecodeCall {
   void* out;               // combined [T][H] (combine) or per-assignment y [T*K][H] fp16
   int out32;
   bool combine;
+  const float* extra;      // [T][H] fp32 added after the combine (block residual + gated shared
+                           // expert), or null: then the layer's dense shared expert output, if any
 };
 
 // Kernel timing hook (kmoe_profile_begin/end).  prof_events hands out the next event pair of
@@ -126,7 +128,7 @@ namespace kmoe {
 // those of kmoe_forward.
 int forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                  int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
-                 void* stream);
+                 void* stream, const float* extra = nullptr);
 // kmoe_workspace_size for `tokens` tokens of `layer`.
 int workspace_bytes_for(const kmoe_layer* layer, int32_t tokens, size_t* bytes);
 // Records `msg` as the calling thread's last error and returns `code`.
@@ -157,6 +159,14 @@ hipError_t launch_zero_bad_rows(const int32_t* idx, int TK, int E, int H, uint16
 hipError_t launch_combine(const float* y32, const uint16_t* y16, const float* wts, int T, int K, int H,
                           const float* shared, void* out, int out32, hipStream_t s);
 hipError_t launch_shared(const LayerConfig& c, const uint16_t* x, int T, const Work& w, hipStream_t s);
+// MoE block (block.hip): out_a[t][r] (r < ra) and out_b[t][r] (r < rb) = rows of the quantized
+// projections a and b (expert 0 of each, `bits`-bit codes) applied to x [T][H]; fp32.
+hipError_t launch_qlinear(const QProj& a, int ra, const QProj& b, int rb, int bits, bool bf16, const uint16_t* x,
+                          int T, int H, float* out_a, float* out_b, hipStream_t s);
+// extra[t][h] = residual[t][h] + fp16 shared16[t][h] * sigmoid(gate[t]) (each term optional; no gate: 1).
+hipError_t launch_blend_prep(const uint16_t* shared16, const float* gate, const uint16_t* residual, int T, int H,
+                             float* extra, hipStream_t s);
+hipError_t launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t s);
 // Writes the prefill copy of c's experts into `pack` (laid out by pack_layout).
 hipError_t launch_prefill_pack(const LayerConfig& c, uint8_t* pack, hipStream_t s);
 hipError_t launch_dequantize(const LayerConfig& c, int proj, int expert, int row0, int nrows, uint8_t* codes,

@@ -389,6 +389,140 @@ class SparseMoeBlock:
         return out
 
 
+class MoEBlock:
+    """The whole MoE block ``mlp(x)`` of a Qwen-style decoder layer, one C call (kmoe_block_forward):
+
+    router projection over the quantized ``mlp.gate`` -> softmax top-K -> renorm -> the routed
+    experts -> weighted combine, plus the quantized shared expert ``mlp.shared_expert`` gated by
+    ``sigmoid(mlp.shared_expert_gate . x)`` and an optional residual:
+    ``out = (residual + sum_k w_k y_k) + fp16(shared(x)) * sigmoid(gate . x)``
+    (kandiga/metal/moe_block.metal:194-584; the bakan_forward_moe_block step,
+    kandiga/metal/bakan_forward.h:111-140).
+
+    ``router``, ``shared`` and ``shared_gate`` hold device tensors: router ``{"w","s","b"}``
+    ``[E, H]``, shared ``{"gate","up","down"}`` each a ``{"w","s","b"}`` dict, shared_gate
+    ``{"w","s","b"}`` ``[1, H]`` (MLX layout, ``bits``-bit codes, ``scale_dtype`` scales).
+    """
+
+    def __init__(self, experts: QuantizedExperts, router: dict, shared: dict | None = None,
+                 shared_gate: dict | None = None, bits: int = 4, scale_dtype: str = "bf16"):
+        if experts.shared:
+            raise ValueError("the routed experts of a block must not carry a dense shared expert")
+        self.experts = experts
+        self.bits = bits
+        self.scale_dtype = scale_dtype
+        dev = experts.device
+        keep = []
+
+        def qp(d: dict, rows: int) -> _capi.QProjDesc:
+            q = _capi.QProjDesc()
+            t = {k: d[k].to(dev).contiguous() for k in ("w", "s", "b")}
+            for k, v in t.items():
+                _on_device(v, dev, f"block projection {k}")
+            if t["w"].shape[0] != rows:
+                raise ValueError(f"projection has {t['w'].shape[0]} rows, expected {rows}")
+            keep.extend(t.values())
+            q.weight, q.scales, q.biases = t["w"].data_ptr(), t["s"].data_ptr(), t["b"].data_ptr()
+            return q
+
+        H, E = experts.shape.hidden, experts.shape.num_experts
+        d = _capi.BlockDesc()
+        d.routed = experts._handle.value
+        d.router = qp(router, E)
+        self.shared_intermediate = 0
+        if shared:
+            Is = shared["gate"]["w"].shape[0]
+            self.shared_intermediate = Is
+            d.shared_gate_proj = qp(shared["gate"], Is)
+            d.shared_up_proj = qp(shared["up"], Is)
+            d.shared_down_proj = qp(shared["down"], H)
+            d.shared_intermediate = Is
+        if shared_gate:
+            d.shared_expert_gate = qp(shared_gate, 1)
+        d.bits = bits
+        d.scale_dtype = _capi.SCALE_BF16 if scale_dtype == "bf16" else _capi.SCALE_F16
+        h = ctypes.c_void_p()
+        _capi.check(_capi.lib().kmoe_block_create(ctypes.byref(d), ctypes.byref(h)), "kmoe_block_create")
+        self._handle = h
+        self._keep = keep
+        self._ws = None
+        self._ws_tokens = -1
+        self._ws_captured = False
+        self._ws_retired = []
+
+    @classmethod
+    def from_arrays(cls, experts: QuantizedExperts, block: dict, bits: int = 4, scale_dtype: str = "bf16") -> "MoEBlock":
+        """From the ``blk_*`` arrays of :func:`synth.make_block` (numpy or torch)."""
+        dev = experts.device
+
+        def t(a):
+            if isinstance(a, torch.Tensor):
+                return a.to(dev)
+            return torch.from_numpy(a.view(a.dtype.str.replace("u", "i"))).to(dev)
+
+        def proj(name):
+            return {k: t(block[f"{name}_{k}"]) for k in ("w", "s", "b")}
+
+        shared = None
+        if "blk_shared_gate_w" in block:
+            shared = {p: proj(f"blk_shared_{p}") for p in ("gate", "up", "down")}
+        gate = proj("blk_sgate") if "blk_sgate_w" in block else None
+        return cls(experts, proj("blk_router"), shared, gate, bits, scale_dtype)
+
+    def workspace(self, tokens: int) -> torch.Tensor:
+        if tokens > self._ws_tokens:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"block workspace for {tokens} tokens was not reserved before graph capture")
+            n = ctypes.c_size_t()
+            _capi.check(_capi.lib().kmoe_block_workspace_size(self._handle, int(tokens), ctypes.byref(n)),
+                        "kmoe_block_workspace_size")
+            if self._ws is not None and self._ws_captured:
+                self._ws_retired.append(self._ws)
+            self._ws = torch.zeros(max(n.value, 256), dtype=torch.uint8, device=self.experts.device)
+            self._ws_tokens = tokens
+            self._ws_captured = False
+        if torch.cuda.is_current_stream_capturing():
+            self._ws_captured = True
+        return self._ws
+
+    def __call__(self, x: torch.Tensor, residual: torch.Tensor | None = None, return_routing: bool = False,
+                 out_dtype: torch.dtype = torch.float16):
+        E = self.experts
+        if out_dtype not in (torch.float16, torch.float32):
+            raise TypeError("out_dtype must be torch.float16 or torch.float32")
+        _on_device(x, E.device, "x")
+        lead = x.shape[:-1]
+        xf = _check_x(x, E.shape.hidden)
+        T = xf.shape[0]
+        res = None
+        if residual is not None:
+            _on_device(residual, E.device, "residual")
+            res = _check_x(residual, E.shape.hidden)
+            if res.shape[0] != T:
+                raise ValueError("x and residual disagree on the number of tokens")
+        out = torch.empty((T, E.shape.hidden), dtype=out_dtype, device=E.device)
+        idx = w = lg = None
+        if return_routing:
+            idx = torch.empty((T, E.shape.top_k), dtype=torch.int32, device=E.device)
+            w = torch.empty((T, E.shape.top_k), dtype=torch.float32, device=E.device)
+            lg = torch.empty((T, E.shape.num_experts), dtype=torch.float32, device=E.device)
+        ws = self.workspace(T)
+        odt = _capi.OUT_F32 if out_dtype == torch.float32 else _capi.OUT_F16
+        _capi.check(_capi.lib().kmoe_block_forward(self._handle, xf.data_ptr(), _ptr(res), T, out.data_ptr(), odt,
+                                                   _ptr(idx), _ptr(w), _ptr(lg), ws.data_ptr(), ws.numel(),
+                                                   _stream()), "kmoe_block_forward")
+        out = out.reshape(*lead, E.shape.hidden)
+        if return_routing:
+            return out, idx.reshape(*lead, -1), w.reshape(*lead, -1), lg.reshape(*lead, -1)
+        return out
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and _capi._lib is not None:
+            _capi._lib.kmoe_block_destroy(h)
+            self._handle = None
+
+
 def route(logits: torch.Tensor, top_k: int):
     """Top-K experts per token (ties -> lower index) and renormalised softmax weights."""
     _on_device(logits, None, "logits")

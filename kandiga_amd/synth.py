@@ -170,3 +170,31 @@ def make_inputs_torch(shape: LayerShape, tokens: int, seed: int, device, zipf: b
         bias = zipf_expert_bias(shape.num_experts, _rng(seed))
         logits = logits + torch.from_numpy(bias).to(device)[None, :]
     return x, logits.contiguous()
+
+
+# --------------------------------------------------------------------------------------
+# The projections of the MoE block around the routed experts
+# --------------------------------------------------------------------------------------
+def make_block(shape: LayerShape, shared_intermediate: int, seed: int, bits: int = 4, scale_dtype: str = "bf16",
+               shared: bool = True, gated: bool = True) -> dict:
+    """Quantized router ``blk_router_{w,s,b}`` ``[E, H]``, shared expert ``blk_shared_{gate,up,down}_{w,s,b}``
+    (gate/up ``[Is, H]``, down ``[H, Is]``) and shared gate ``blk_sgate_{w,s,b}`` ``[1, H]`` in the MLX
+    layout with ``bits``-bit codes (the distributions of :func:`make_layer`, without the expert
+    dimension)."""
+    rng = _rng(seed)
+    H, E, Is = shape.hidden, shape.num_experts, shared_intermediate
+    out = {}
+    projs = [("blk_router", E, H)]
+    if shared:
+        projs += [("blk_shared_gate", Is, H), ("blk_shared_up", Is, H), ("blk_shared_down", H, Is)]
+        if gated:
+            projs += [("blk_sgate", 1, H)]
+    for name, rows, cols in projs:
+        out[f"{name}_w"] = rng.integers(0, 2 ** 32, size=(rows, packed_row_words(cols, bits)), dtype=np.uint32)
+        sc = _scales_f16_bits(rng, (rows, cols // GROUP_SIZE))
+        bi = f16_bits(sc.view(np.float16).astype(np.float32) * np.float32(-(2 ** (bits - 1))))
+        if scale_dtype == "bf16":
+            sc, bi = f16_to_bf16_bits(sc), f16_to_bf16_bits(bi)
+        out[f"{name}_s"] = sc
+        out[f"{name}_b"] = bi
+    return out

@@ -389,6 +389,57 @@ def moe_layer(layer: dict, x: np.ndarray, logits: np.ndarray, top_k: int, bits: 
     return dict(idx=idx, w=w, y=y, out=out)
 
 
+def qlinear_f64(words, scales, biases, bits: int, x: np.ndarray, scale_dtype: str = "f16") -> np.ndarray:
+    """``x @ W.T`` for a group-quantized projection ``W [rows, in]`` (MLX layout), float64 (the
+    router and shared-gate projections, moe_block.metal:194-227, 300-336)."""
+    xs = np.atleast_2d(np.asarray(x, dtype=np.float16).astype(np.float64))
+    w = dequantize(words, scales, biases, bits, xs.shape[1], scale_dtype)
+    return xs @ w.T
+
+
+def block_shared_layer(block: dict) -> dict:
+    """The block's quantized shared expert as a one-expert stacked layer dict."""
+    return {f"{p}_{k}": np.ascontiguousarray(block[f"blk_shared_{p}_{k}"][None]) for p in ("gate", "up", "down")
+            for k in ("w", "s", "b")}
+
+
+def moe_block(layer: dict, block: dict, x: np.ndarray, top_k: int, bits: int, block_bits: int,
+              scale_dtype: str = "f16", block_scale_dtype: str = "bf16", residual=None, logits=None,
+              nthreads: int = 1) -> dict:
+    """The whole MoE block (moe_block.metal:194-584; bakan_forward.h:111-140):
+
+    logits = router . x (fp32); softmax -> top-K -> renorm; the routed experts' weighted sum
+    (C restatement, fp32, k order); the shared expert (C restatement) rounded to fp16 as the
+    reference's shared_expert_down_kernel stores it (:324); its gate sigmoid(shared_gate . x);
+    out = (residual + routed) + shared16 * gate (:577-583; without a residual :536-538).
+    ``logits`` given: route on those instead (to check the rest of the block on a device's
+    own logits)."""
+    lg = qlinear_f64(block["blk_router_w"], block["blk_router_s"], block["blk_router_b"], block_bits, x,
+                     block_scale_dtype).astype(np.float32)
+    use = lg if logits is None else np.asarray(logits, dtype=np.float32)
+    idx, w = route(use, top_k)
+    out = combine(switch_mlp(layer, x, idx, bits, scale_dtype, nthreads=nthreads), w).astype(np.float64)
+    if residual is not None:
+        out = np.asarray(residual, dtype=np.float16).astype(np.float64) + out
+    if "blk_shared_gate_w" in block:
+        T = np.atleast_2d(x).shape[0]
+        sh = switch_mlp(block_shared_layer(block), x, np.zeros((T, 1), np.int32), block_bits, block_scale_dtype)[:, 0]
+        sh16 = round_f16(sh).astype(np.float64)
+        g = np.ones((T, 1))
+        if "blk_sgate_w" in block:
+            gl = qlinear_f64(block["blk_sgate_w"], block["blk_sgate_s"], block["blk_sgate_b"], block_bits, x,
+                             block_scale_dtype)
+            g = 1.0 / (1.0 + np.exp(-gl))
+        out = out + sh16 * g
+        # one fp16 spacing of the shared output, gated: how far a device whose fp32 shared value
+        # differs in the last bits can land after the fp16 rounding
+        a = np.maximum(np.abs(sh).astype(np.float64), 2.0 ** -14)
+        flip = np.exp2(np.floor(np.log2(a)) - 10) * g
+    else:
+        flip = np.zeros_like(out)
+    return dict(logits=lg, idx=idx, w=w, out=out.astype(np.float32), shared_flip=flip)
+
+
 def compare(got: np.ndarray, ref: np.ndarray) -> dict:
     """max-abs and relative-L2 error of ``got`` against ``ref`` (both taken as float64)."""
     g = np.asarray(got, dtype=np.float64)

@@ -369,3 +369,50 @@ def test_ref_scalar_baseline_computes_the_same_layer(bits, scale_dtype):
     for nt in (1, 4):
         got = O.ref_scalar_switch_mlp(layer, x, idx, bits, scale_dtype, nthreads=nt)
         assert O.compare(got, ref)["rel_l2"] < 1e-5
+
+
+# ---- the MoE block around the routed experts ----------------------------------------------
+def test_qlinear_brute_force():
+    """qlinear_f64 against explicit loops over rows, columns and the bit stream."""
+    rng = np.random.default_rng(41)
+    for bits in (3, 4):
+        rows, cols = 5, 128
+        codes = rng.integers(0, 2 ** bits, size=(rows, cols))
+        w = layout.pack_codes(codes, bits)
+        s = layout.f16_bits((rng.random((rows, 2)) * 0.1 + 0.01).astype(np.float16))
+        b = layout.f16_bits((rng.standard_normal((rows, 2)) * 0.1).astype(np.float16))
+        x = rng.standard_normal((3, cols)).astype(np.float16)
+        got = O.qlinear_f64(w, s, b, bits, x)
+        for t in range(3):
+            for r in range(rows):
+                acc = 0.0
+                for c in range(cols):
+                    wv = codes[r, c] * float(s.view(np.float16)[r, c // 64]) + float(b.view(np.float16)[r, c // 64])
+                    acc += wv * float(x[t, c])
+                assert abs(got[t, r] - acc) <= 1e-9 * max(1.0, abs(acc))
+
+
+def test_moe_block_composition_closed_form():
+    """Zero router weights make every logit 0 (route: experts 0..K-1, weights 1/K) and a zero
+    shared gate makes sigmoid = 1/2: out = residual + mean_k y_k + fp16(shared) / 2.  Dropping
+    the residual, the gate or the fp16 rounding of the shared output changes the value."""
+    shape = synth.LayerShape(128, 64, 6, 3, 3)
+    layer = synth.make_layer(shape, 43)
+    blk = synth.make_block(shape, 64, 44, bits=4, scale_dtype="bf16")
+    mid = layout.f32_to_bf16_bits(np.float32([0.0]))[0]
+    for name in ("blk_router", "blk_sgate"):
+        blk[f"{name}_w"][:] = 0          # codes 0 ...
+        blk[f"{name}_b"][:] = mid         # ... and zero bias: every weight is 0
+    x, _ = synth.make_inputs(shape, 4, 45)
+    res = (np.random.default_rng(46).standard_normal((4, 128)) * 3).astype(np.float16)
+    r = O.moe_block(layer, blk, x, 3, 3, 4, "f16", "bf16", residual=res)
+    assert np.array_equal(r["idx"], np.tile(np.arange(3, dtype=np.int32), (4, 1)))
+    np.testing.assert_allclose(r["w"], 1 / 3, rtol=1e-6)
+    y = O.switch_mlp(layer, x, r["idx"], 3)
+    sh = O.switch_mlp(O.block_shared_layer(blk), x, np.zeros((4, 1), np.int32), 4, "bf16")[:, 0]
+    sh16 = O.round_f16(sh).astype(np.float64)
+    want = res.astype(np.float64) + y.astype(np.float64).mean(axis=1) + 0.5 * sh16
+    np.testing.assert_allclose(r["out"], want, rtol=2e-6, atol=2e-6)
+    assert np.abs(sh16 - sh).max() > 0                       # the shared output is rounded
+    assert np.abs(r["out"] - (want - res)).max() > 1.0       # the residual is in
+    assert np.abs(0.5 * sh16).max() > 1e-2                   # the gated shared term matters
