@@ -200,6 +200,30 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
                        size_t workspace_bytes, void* stream);
 
 /*
+ * TQ3 codebook weights (kandiga/tq3/quantize.py:120-143, 390-486): 32 weights per 20-byte block
+ * (fp16 d0 d1 m0 m1, 12 bytes of 3-bit Lloyd-Max indices), w = iWHT(C[q]*d + m) per block; a
+ * matrix [rows][cols] is its rows' blocks in order.
+ *
+ * kmoe_tq3_gemv: out[t][r] = sum_c W[r][c] x[t][c], fp32, the input rotated into the transform
+ * domain once per 32-block (replaces tq3_gemv, kandiga/tq3/fused_kernel.py:170-251, and
+ * tq3_matvec / tq3_rotate_activations, kandiga/tq3/tq3_metal.metal:55-141).
+ *   blocks device [rows*cols/32][20]; x device [tokens][cols] fp16 (x_f32 = 0) or fp32 (1);
+ *   out device fp32 [tokens][rows]; cols a multiple of 32 up to 4096.
+ *
+ * kmoe_tq3_expert_mlp: the switch_mlp contract over TQ3 experts (a TQ3X file body,
+ * kandiga/tq3/convert_experts.py:140-200: per expert the gate [I][H], up [I][H] and down [H][I]
+ * matrices in turn, expert_bytes apart): y[t][k] = down(silu(gate x_t) * (up x_t)) of expert
+ * idx[t][k], fp16.  Experts outside [0, num_experts) give zero rows.  The workspace holds the
+ * gate/up outputs (kmoe_tq3_workspace_size).
+ */
+int kmoe_tq3_gemv(const void* blocks, int32_t rows, int32_t cols, const void* x, int32_t x_f32, int32_t tokens,
+                  float* out, void* stream);
+int kmoe_tq3_workspace_size(int32_t tokens, int32_t top_k, int32_t intermediate, size_t* bytes);
+int kmoe_tq3_expert_mlp(const void* experts, int64_t expert_bytes, int32_t num_experts, int32_t hidden,
+                        int32_t intermediate, const void* x, const int32_t* idx, int32_t tokens, int32_t top_k, void* y,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * kmoe_forward without a workspace argument: the library's own static device scratch of
  * KMOE_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends) serves as the workspace, and
  * the call allocates nothing (no hipMalloc, no allocating library routine).  No counterpart in

@@ -20,6 +20,7 @@ EXPORTS = (
     "kmoe_route", "kmoe_permute_workspace_size", "kmoe_permute",
     "kmoe_expert_mlp", "kmoe_combine", "kmoe_forward",
     "kmoe_block_create", "kmoe_block_destroy", "kmoe_block_workspace_size", "kmoe_block_forward",
+    "kmoe_tq3_gemv", "kmoe_tq3_workspace_size", "kmoe_tq3_expert_mlp",
     "kmoe_forward_noalloc",
     "kmoe_prefill_pack_size", "kmoe_prefill_pack",
     "kmoe_dequantize", "kmoe_device_status",
@@ -95,6 +96,10 @@ def _declare(L):
         "kmoe_block_destroy": ([_vp], ctypes.c_int),
         "kmoe_block_workspace_size": ([_vp, _i32, P(_sz)], ctypes.c_int),
         "kmoe_block_forward": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
+        "kmoe_tq3_gemv": ([_vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
+        "kmoe_tq3_workspace_size": ([_i32, _i32, _i32, P(_sz)], ctypes.c_int),
+        "kmoe_tq3_expert_mlp": ([_vp, ctypes.c_int64, _i32, _i32, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _sz, _vp],
+                                ctypes.c_int),
         "kmoe_forward_noalloc": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp], ctypes.c_int),
         "kmoe_prefill_pack_size": ([P(LayerDesc), P(_sz)], ctypes.c_int),
         "kmoe_prefill_pack": ([P(LayerDesc), _vp, _sz, _vp], ctypes.c_int),

@@ -516,6 +516,60 @@ int kmoe_profile_end(kmoe_kernel_time* entries, int32_t max_entries, int32_t* n_
 
 }  // extern "C"
 
+// ---- TQ3 codebook experts ------------------------------------------------------------------
+extern "C" {
+
+int kmoe_tq3_gemv(const void* blocks, int32_t rows, int32_t cols, const void* x, int32_t x_f32, int32_t tokens,
+                  float* out, void* stream) {
+  if (rows < 0 || tokens < 0 || cols <= 0 || cols % 32 || cols > 4096)
+    return fail(KMOE_ERR_INVALID_ARG, "rows/tokens must be >= 0 and cols a multiple of 32 up to 4096");
+  if (rows == 0 || tokens == 0) return ok();
+  if (!blocks || !x || !out) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
+  if (!aligned(blocks, 4) || !aligned(x, 4) || !aligned(out, 4)) return fail(KMOE_ERR_ALIGNMENT, "pointers must be 4-byte aligned");
+  Tq3Params p{static_cast<const uint8_t*>(blocks), 0, 0, 0, rows, nullptr, 1, x, 1, tokens, rows, cols, out, nullptr};
+  hipError_t e = launch_tq3_gemv(p, x_f32 ? 1 : 0, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "tq3 gemv launch");
+}
+
+int kmoe_tq3_workspace_size(int32_t tokens, int32_t top_k, int32_t intermediate, size_t* bytes) {
+  if (!bytes || tokens < 0 || top_k < 1 || intermediate <= 0) return fail(KMOE_ERR_INVALID_ARG, "bad sizes");
+  *bytes = up256((size_t)tokens * top_k * 2 * intermediate * sizeof(float));
+  return ok();
+}
+
+int kmoe_tq3_expert_mlp(const void* experts, int64_t expert_bytes, int32_t num_experts, int32_t hidden,
+                        int32_t intermediate, const void* x, const int32_t* idx, int32_t tokens, int32_t top_k, void* y,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  if (num_experts < 1 || top_k < 1 || tokens < 0 || hidden <= 0 || intermediate <= 0 || hidden % 32 ||
+      intermediate % 32 || hidden > 4096 || intermediate > 4096)
+    return fail(KMOE_ERR_INVALID_ARG, "hidden/intermediate must be multiples of 32 up to 4096; E, K >= 1");
+  const int64_t mat = (int64_t)hidden * intermediate / 32 * 20;
+  if (expert_bytes < 3 * mat) return fail(KMOE_ERR_INVALID_ARG, "expert_bytes below the three TQ3 matrices");
+  if (tokens == 0) return ok();
+  if (!experts || !x || !idx || !y || !workspace) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
+  if (!aligned(experts, 4) || expert_bytes % 4 || !aligned(x, 4) || !aligned(y, 4) || !aligned(idx, 4) ||
+      !aligned(workspace, 4))
+    return fail(KMOE_ERR_ALIGNMENT, "pointers and expert_bytes must be 4-byte aligned");
+  size_t need = 0;
+  kmoe_tq3_workspace_size(tokens, top_k, intermediate, &need);
+  if (workspace_bytes < need) return fail(KMOE_ERR_WORKSPACE, "workspace has %zu bytes, needs %zu", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* gu = static_cast<float*>(workspace);
+  const uint8_t* w = static_cast<const uint8_t*>(experts);
+  const int V = tokens * top_k;
+  // gate rows then up rows of every (token, k), gate/up pairs [V][2I] fp32
+  Tq3Params a{w, expert_bytes, 0, mat, intermediate, idx, num_experts, x, top_k, V, 2 * intermediate, hidden, gu,
+              nullptr};
+  hipError_t e = launch_tq3_gemv(a, 0, s);
+  // down projection of silu(g)*u, fp16 y [V][H]
+  Tq3Params d{w, expert_bytes, 2 * mat, 2 * mat, hidden, idx, num_experts, gu, 1, V, hidden, intermediate, nullptr,
+              static_cast<uint16_t*>(y)};
+  if (e == hipSuccess) e = launch_tq3_gemv(d, 2, s);
+  return e == hipSuccess ? ok() : hip_fail(e, "tq3 expert mlp launch");
+}
+
+}  // extern "C"
+
 // ---- the MoE block around the routed experts ------------------------------------------------
 struct kmoe_block {
   const kmoe_layer* routed;
