@@ -43,10 +43,10 @@ enum { KMOE_SCALE_F16 = 0, KMOE_SCALE_BF16 = 1 };
 enum { KMOE_ACT_SWIGLU = 0, KMOE_ACT_GELU_TANH = 1 };
 enum { KMOE_PROJ_GATE = 0, KMOE_PROJ_UP = 1, KMOE_PROJ_DOWN = 2 };
 enum { KMOE_OUT_F16 = 0, KMOE_OUT_F32 = 1 };
-/* Device error flags reported by kmoe_device_status. */
+/* Device error flags reported by kmoe_device_status (other bits are reserved and read 0: no
+   kernel waits on another workgroup, so there is no time-out to report). */
 enum {
-  KMOE_DEVERR_BAD_EXPERT = 1, /* an expert index outside [0, num_experts) was dropped */
-  KMOE_DEVERR_SPIN = 2        /* a grid-wide wait of the decode kernel reached its bound */
+  KMOE_DEVERR_BAD_EXPERT = 1 /* an expert index outside [0, num_experts) was dropped */
 };
 
 typedef struct {

@@ -35,7 +35,6 @@ ACT_SWIGLU, ACT_GELU_TANH = 0, 1
 OUT_F16, OUT_F32 = 0, 1
 DEVERR_BAD_EXPERT = 1
 NOALLOC_SCRATCH_BYTES = 16 << 20
-DEVERR_SPIN = 2
 
 
 class KmoeError(RuntimeError):

@@ -83,7 +83,6 @@ constexpr int DEC_STAGE2_ASSIGN = 128; // assignments held in two lane slots by 
 
 // Device error flag bits (Work::scalars[2]).
 constexpr int DEVERR_BAD_EXPERT = 1;
-constexpr int DEVERR_SPIN = 2;  // a grid-wide wait reached its spin bound
 
 // One decode-path call (1..DEC_MAX_TOKENS tokens): routing from logits, or given indices.
 struct DecodeCall {

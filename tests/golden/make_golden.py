@@ -2,8 +2,10 @@
 per-(token, k) expert outputs and combined layer output, all computed by the oracle.
 
 The reference's own tests hold no vectors for this path, and its expert-MLP sources need
-Apple headers this image lacks, so these fixtures pin the oracle against drift (and give the
-GPU tests a stored target); the oracle itself is pinned by tests/test_oracle.py.
+Apple headers this image lacks, so these fixtures pin the oracle against drift
+(tests/test_oracle.py::test_golden_fixture_reproduces) and give the GPU path a stored target
+(tests/test_gpu_parity.py::test_stored_golden_fixture); the oracle itself is pinned by the
+other tests in tests/test_oracle.py.
 Only the layer's SHA-256 is stored, not the weights: the generator recreates them.
 
 Run:  python -m tests.golden.make_golden

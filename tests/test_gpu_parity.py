@@ -344,6 +344,31 @@ def test_combine_matches_closed_form(device):
 
 
 # ---- benchmark-sized layers -------------------------------------------------------------
+@pytest.mark.parametrize("name", ["h256_e16_i128_k4_3bit", "h256_e16_i128_k4_4bit", "h320_e12_i192_k3_3bit"])
+def test_stored_golden_fixture(device, name):
+    """The stored fixture (tests/golden/moe_small.npz): its inputs through the HIP path give its
+    stored routing bit for bit, its stored per-(token, k) expert outputs and its combined output
+    (layers regenerated from the seed, checked against the stored SHA-256)."""
+    import os
+
+    from kandiga_amd.moe import QuantizedExperts, QuantizedSwitchGLU, SparseMoeBlock
+    from tests.golden.make_golden import CASES, layer_sha256
+
+    data = np.load(os.path.join(os.path.dirname(__file__), "golden", "moe_small.npz"))
+    shape, seed, _tokens = CASES[name]
+    layer = synth.make_layer(shape, seed)
+    assert layer_sha256(layer) == str(data[f"{name}.layer_sha256"])
+    ex = QuantizedExperts.from_stacked(shape, layer, device)
+    x = torch.from_numpy(data[f"{name}.x"]).to(device)
+    lg = torch.from_numpy(data[f"{name}.logits"]).to(device)
+    out, idx, w = SparseMoeBlock(ex)(x, lg, return_routing=True)
+    assert np.array_equal(to_np(idx), data[f"{name}.idx"])
+    np.testing.assert_allclose(to_np(w), data[f"{name}.w"], rtol=2e-6, atol=2e-7)
+    y = QuantizedSwitchGLU(ex)(x, idx)
+    assert_close(to_np(y), data[f"{name}.y"], what=f"{name} stored y")
+    assert_close(to_np(out), data[f"{name}.out"], what=f"{name} stored out")
+
+
 @pytest.fixture(scope="module")
 def full3(device):
     shape = synth.SHAPES["h2048-e256-i512-k8-3bit"]
