@@ -21,4 +21,13 @@ Pins (each function's docstring names its checks in ``tests/``):
                         GELU-tanh mode against ``torch.nn.functional.gelu(approximate='tanh')``.
 * ``shared_expert_f64`` closed form for constant matrices (with a gate/up swap that must
                         differ) and explicit index loops on non-square matrices.
+* ``qlinear_f64``       brute-force loops over the quantized rows.
+* ``moe_block``         the block composition against a closed form with constant shared
+                        weights.
+* ``ref_scalar`` (C)    the same layer as ``switch_mlp`` within fp32 rounding.
+* ``tq3_oracle``        Hadamard identities (H H = 32 I, inverse of forward, the dot identity),
+                        the sign table's defining hash, centroid/boundary consistency, a
+                        constant block's closed form, index packing, and the reference
+                        quantizer's own blocks and dequantized weights
+                        (tests/golden/tq3_quantize.npz).
 """
