@@ -43,6 +43,8 @@ enum { KMOE_SCALE_F16 = 0, KMOE_SCALE_BF16 = 1 };
 enum { KMOE_ACT_SWIGLU = 0, KMOE_ACT_GELU_TANH = 1 };
 enum { KMOE_PROJ_GATE = 0, KMOE_PROJ_UP = 1, KMOE_PROJ_DOWN = 2 };
 enum { KMOE_OUT_F16 = 0, KMOE_OUT_F32 = 1 };
+/* Activation dtypes of kmoe_expert_mlp_x / kmoe_forward_x. */
+enum { KMOE_X_F16 = 0, KMOE_X_BF16 = 1, KMOE_X_F32 = 2 };
 /* Device error flags reported by kmoe_device_status (other bits are reserved and read 0: no
    kernel waits on another workgroup, so there is no time-out to report). */
 enum {
@@ -131,6 +133,20 @@ int kmoe_permute(const int32_t* idx, int32_t tokens, int32_t top_k, int32_t num_
  */
 int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, int32_t tokens, void* y,
                     void* workspace, size_t workspace_bytes, void* stream);
+/*
+ * kmoe_expert_mlp with the activations in the caller's dtype: x_dtype KMOE_X_F16, KMOE_X_BF16 or
+ * KMOE_X_F32 (rows [tokens][H]).  Replaces bakan_cpu_expert_mlp_bf16 (bf16 x) and
+ * bakan_cpu_expert_mlp (fp32 x) (kandiga/metal/kandiga_cpu_expert.h:51-89,
+ * kandiga_cpu_expert.m:471-552, 690-719), which widen x to fp32.  Each token's row is taken as
+ * fp16 planes of x * 2^s: s = 0 when its largest magnitude m lies in [2^-4, 2^4), else the power
+ * of two that puts m in [1, 2).  A bf16 row is then exact in the hi plane (elements down to
+ * 2^-14 m), an fp32 row carries ~22 bits (hi + lo planes); gate/up are multiplied by 2^-s and
+ * the SwiGLU output is carried times 2^2s and taken back after the down projection, all exact
+ * in fp32, so rows far outside fp16's range stay in range.  Rows of fp16-representable values
+ * with m in the window give the fp16 path's result bit for bit.
+ */
+int kmoe_expert_mlp_x(const kmoe_layer* layer, const void* x, int32_t x_dtype, const int32_t* idx, int32_t tokens,
+                      void* y, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Weighted combine of switch_mlp outputs: out[t] = sum_k weights[t][k] * y[t][k], fp32
@@ -155,6 +171,11 @@ int kmoe_combine(const void* y, const float* weights, int32_t tokens, int32_t to
 int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                  int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
                  void* stream);
+/* kmoe_forward with the activations in the caller's dtype (as kmoe_expert_mlp_x).  A layer with
+ * the dense fp16 shared expert takes KMOE_X_F16 only (KMOE_ERR_UNSUPPORTED otherwise). */
+int kmoe_forward_x(const kmoe_layer* layer, const void* x, int32_t x_dtype, const float* logits, int32_t tokens,
+                   void* out, int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 /*
  * The whole MoE block mlp(x) of the decoder layer: router projection over the quantized

@@ -18,7 +18,7 @@ EXPORTS = (
     "kmoe_version", "kmoe_strerror", "kmoe_last_error",
     "kmoe_layer_create", "kmoe_layer_destroy", "kmoe_workspace_size",
     "kmoe_route", "kmoe_permute_workspace_size", "kmoe_permute",
-    "kmoe_expert_mlp", "kmoe_combine", "kmoe_forward",
+    "kmoe_expert_mlp", "kmoe_expert_mlp_x", "kmoe_combine", "kmoe_forward", "kmoe_forward_x",
     "kmoe_block_create", "kmoe_block_destroy", "kmoe_block_workspace_size", "kmoe_block_forward",
     "kmoe_tq3_gemv", "kmoe_tq3_workspace_size", "kmoe_tq3_expert_mlp",
     "kmoe_forward_noalloc",
@@ -33,6 +33,7 @@ ERR_HIP, ERR_IO, ERR_FORMAT, ERR_DEVICE, ERR_NO_MEMORY = -5, -6, -7, -8, -9
 SCALE_F16, SCALE_BF16 = 0, 1
 ACT_SWIGLU, ACT_GELU_TANH = 0, 1
 OUT_F16, OUT_F32 = 0, 1
+X_F16, X_BF16, X_F32 = 0, 1, 2
 DEVERR_BAD_EXPERT = 1
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
@@ -89,8 +90,10 @@ def _declare(L):
         "kmoe_permute_workspace_size": ([_i32, _i32, _i32, P(_sz)], ctypes.c_int),
         "kmoe_permute": ([_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
         "kmoe_expert_mlp": ([_vp, _vp, _vp, _i32, _vp, _vp, _sz, _vp], ctypes.c_int),
+        "kmoe_expert_mlp_x": ([_vp, _vp, _i32, _vp, _i32, _vp, _vp, _sz, _vp], ctypes.c_int),
         "kmoe_combine": ([_vp, _vp, _i32, _i32, _i32, _vp, _vp], ctypes.c_int),
         "kmoe_forward": ([_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
+        "kmoe_forward_x": ([_vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _sz, _vp], ctypes.c_int),
         "kmoe_block_create": ([P(BlockDesc), P(_vp)], ctypes.c_int),
         "kmoe_block_destroy": ([_vp], ctypes.c_int),
         "kmoe_block_workspace_size": ([_vp, _i32, P(_sz)], ctypes.c_int),

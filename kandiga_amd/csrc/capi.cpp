@@ -95,9 +95,10 @@ Work carve(char* base, int T, int K, int E, int H, int I, int Is, bool need_y, s
   w.mt_row0 = reinterpret_cast<int32_t*>(take((size_t)mmt * 4));
   w.mt_rows = reinterpret_cast<int32_t*>(take((size_t)mmt * 4));
   w.act = reinterpret_cast<uint16_t*>(take(TK * I * 2 * 2));  // hi and lo planes
+  w.xinv = reinterpret_cast<float*>(take((size_t)T * 4));
   if (need_y) {
     w.y32 = reinterpret_cast<float*>(take(TK * H * 4));
-    w.xpp = reinterpret_cast<uint16_t*>(take((size_t)T * H * 2));
+    w.xpp = reinterpret_cast<uint16_t*>(take((size_t)T * H * 2 * 2));  // hi and lo planes
   }
   if (Is > 0) {
     w.shared_out = reinterpret_cast<float*>(take((size_t)T * H * 4));
@@ -333,7 +334,13 @@ int kmoe_permute(const int32_t* idx, int32_t tokens, int32_t top_k, int32_t num_
 
 int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, int32_t tokens, void* y,
                     void* workspace, size_t workspace_bytes, void* stream) {
+  return kmoe_expert_mlp_x(layer, x, KMOE_X_F16, idx, tokens, y, workspace, workspace_bytes, stream);
+}
+
+int kmoe_expert_mlp_x(const kmoe_layer* layer, const void* x, int32_t x_dtype, const int32_t* idx, int32_t tokens,
+                      void* y, void* workspace, size_t workspace_bytes, void* stream) {
   if (!layer) return fail(KMOE_ERR_INVALID_ARG, "null layer");
+  if (x_dtype < KMOE_X_F16 || x_dtype > KMOE_X_F32) return fail(KMOE_ERR_INVALID_ARG, "unknown x_dtype %d", x_dtype);
   if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
   if (tokens == 0) return ok();
   if (!x || !idx || !y || !workspace) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
@@ -345,17 +352,17 @@ int kmoe_expert_mlp(const kmoe_layer* layer, const void* x, const int32_t* idx, 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const LayerConfig& c = layer->cfg;
   const int K = c.top_k;
-  const uint16_t* xx = static_cast<const uint16_t*>(x);
   uint16_t* yy = static_cast<uint16_t*>(y);
   hipError_t e;
   if (is_decode(tokens, K, c.args.H)) {
-    DecodeCall d{xx, nullptr, idx, tokens, nullptr, nullptr, nullptr, &w, yy, 0, false, nullptr};
+    DecodeCall d{x, nullptr, idx, tokens, nullptr, nullptr, nullptr, &w, yy, 0, false, nullptr, x_dtype};
     e = launch_decode(c, d, s);
   } else {
-    const int bm = gemm_bm(c.args), mmt = max_mtiles_for(tokens * K, c.args.E, bm);
+    const int bm = gemm_bm(c.args, x_dtype), mmt = max_mtiles_for(tokens * K, c.args.E, bm);
     e = launch_permute(idx, tokens * K, K, c.args.E, w, mmt, bm, s);
-    if (e == hipSuccess) e = launch_xpair(c, xx, tokens, w.xpp, s);
-    if (e == hipSuccess) e = launch_gemm(c, w.xpp, tokens, w, mmt, yy, nullptr, s);
+    if (e == hipSuccess) e = launch_xpair(c, x, x_dtype, tokens, w.xpp, w.xinv, s);
+    if (e == hipSuccess)
+      e = launch_gemm(c, w.xpp, tokens, w, mmt, yy, nullptr, s, x_dtype, x_dtype == KMOE_X_F16 ? nullptr : w.xinv);
     if (e == hipSuccess) e = launch_zero_bad_rows(idx, tokens * K, c.args.E, c.args.H, yy, s);
   }
   return e == hipSuccess ? ok() : hip_fail(e, "expert_mlp launch");
@@ -381,13 +388,21 @@ int kmoe_forward(const kmoe_layer* layer, const void* x, const float* logits, in
                             workspace_bytes, stream);
 }
 
+int kmoe_forward_x(const kmoe_layer* layer, const void* x, int32_t x_dtype, const float* logits, int32_t tokens,
+                   void* out, int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  if (x_dtype < KMOE_X_F16 || x_dtype > KMOE_X_F32) return fail(KMOE_ERR_INVALID_ARG, "unknown x_dtype %d", x_dtype);
+  return kmoe::forward_impl(layer, x, logits, tokens, out, out_dtype, idx_out, weights_out, workspace,
+                            workspace_bytes, stream, nullptr, x_dtype);
+}
+
 }  // extern "C"
 
 // The routed layer on a caller-provided workspace (kmoe_forward, and kmoe_forward_noalloc with the
 // library's static scratch).
 int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                        int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace,
-                       size_t workspace_bytes, void* stream, const float* extra) {
+                       size_t workspace_bytes, void* stream, const float* extra, int xdt) {
   if (!layer) return fail(KMOE_ERR_INVALID_ARG, "null layer");
   if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
   if (out_dtype != KMOE_OUT_F16 && out_dtype != KMOE_OUT_F32) return fail(KMOE_ERR_INVALID_ARG, "unknown out_dtype");
@@ -405,20 +420,22 @@ int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logi
   const LayerConfig& c = layer->cfg;
   const LayerArgs& a = c.args;
   const int K = c.top_k;
+  if (a.sh_gate && xdt != KMOE_X_F16)
+    return fail(KMOE_ERR_UNSUPPORTED, "the dense shared expert takes fp16 activations only");
   if (idx_out) w.idx = idx_out;
   if (weights_out) w.wts = weights_out;
-  const uint16_t* xx = static_cast<const uint16_t*>(x);
   hipError_t e = hipSuccess;
-  if (a.sh_gate) e = launch_shared(c, xx, tokens, w, s);
+  if (a.sh_gate) e = launch_shared(c, static_cast<const uint16_t*>(x), tokens, w, s);
   if (e != hipSuccess) return hip_fail(e, "shared expert launch");
   if (is_decode(tokens, K, a.H)) {
-    DecodeCall d{xx, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true, extra};
+    DecodeCall d{x, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true, extra, xdt};
     e = launch_decode(c, d, s);
   } else {
-    const int bm = gemm_bm(a), mmt = max_mtiles_for(tokens * K, a.E, bm);
-    e = launch_route_xpair(logits, tokens, a.E, K, w.idx, w.wts, xx, a.H, c.bits, w.xpp, s);
+    const int bm = gemm_bm(a, xdt), mmt = max_mtiles_for(tokens * K, a.E, bm);
+    e = launch_route_xpair(logits, tokens, a.E, K, w.idx, w.wts, x, xdt, a.H, c.bits, w.xpp, w.xinv, s);
     if (e == hipSuccess) e = launch_permute(w.idx, tokens * K, K, a.E, w, mmt, bm, s);
-    if (e == hipSuccess) e = launch_gemm(c, w.xpp, tokens, w, mmt, nullptr, w.wts, s);
+    if (e == hipSuccess)
+      e = launch_gemm(c, w.xpp, tokens, w, mmt, nullptr, w.wts, s, xdt, xdt == KMOE_X_F16 ? nullptr : w.xinv);
     if (e == hipSuccess)
       e = launch_combine(w.y32, nullptr, nullptr, tokens, K, a.H, extra ? extra : a.sh_gate ? w.shared_out : nullptr,
                          out, out32, s);
@@ -723,7 +740,7 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
     } else if (e == hipSuccess) {
       const int bm = gemm_bm(sc.args), mmt = max_mtiles_for(tokens, 1, bm);
       e = launch_permute(w.idx0, tokens, 1, 1, w.sh, mmt, bm, s);
-      if (e == hipSuccess) e = launch_xpair(sc, xx, tokens, w.sh.xpp, s);
+      if (e == hipSuccess) e = launch_xpair(sc, xx, KMOE_X_F16, tokens, w.sh.xpp, nullptr, s);
       if (e == hipSuccess) e = launch_gemm(sc, w.sh.xpp, tokens, w.sh, mmt, w.ysh, nullptr, s);
     }
   }

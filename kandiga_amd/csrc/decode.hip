@@ -23,6 +23,11 @@
 //     go to LDS and are combined in k order with the routing weights (moe_block.metal:515-539),
 //     so the fused combine is deterministic.  The per-assignment variant writes y[t,k,:]
 //     instead (the switch_mlp contract, engine.py:670-739).
+// No implicit multiply-add contraction in this file (explicit fmaf where a fused product is
+// meant): the fp16 and the scaled-activation instantiations of stage 1 inline the same
+// expressions into different code, and fp16-representable rows must give the same bits in both.
+#pragma clang fp contract(off)
+
 #include "kmoe_device.h"
 #include "kmoe_internal.h"
 
@@ -100,7 +105,8 @@ __device__ __forceinline__ void load16(const void* p, uint32_t (&v)[16]) {
 
 struct Stage1Args {
   LayerArgs L;
-  const uint16_t* x;        // [T][H]
+  const void* x;            // [T][H] of dtype xdt (fp16, bf16, fp32)
+  int xdt;
   const float* logits;      // [T][E] (routing mode) or null
   const int32_t* idx_in;    // [T][K] (given-indices mode) or null
   int T, K;
@@ -109,6 +115,7 @@ struct Stage1Args {
   int32_t* scalars;         // [2] = device error flags
   uint16_t* act;            // [2][T*K][I], row a = assignment t*K + k
   size_t act_plane;
+  float* xinv;              // [T] 2^-s of scaled activations (bf16 / fp32), or null
   int wgs_per_expert;       // row blocks (items) per expert: I / (4*RW)
   int wgs_per_token;        // workgroups working on each token
 };
@@ -125,8 +132,11 @@ struct Stage1Args {
 // and the lane's chunk offset a constant.  Tokens are not grouped by expert: routing one token per
 // workgroup keeps the prologue as short as a single token's, and an expert that two tokens share
 // is read twice (the second read mostly from the memory-side cache).  CPL = x chunks per lane
-// (H <= 64*32*CPL).
-template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE>
+// (H <= 64*32*CPL).  bf16 and fp32 activations are scaled per token (kmoe_device.h, scaled
+// activations): the dots run on the scaled hi plane (and, for fp32, the lo plane as a second
+// dot), the gate/up totals are multiplied by 2^-s before the activation, act is stored times
+// 2^2s, and 2^-s goes to xinv[t] for stage 2.
+template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE, bool XS>
 __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   const LayerArgs& L = A.L;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -135,15 +145,38 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   const int t = blockIdx.x / A.wgs_per_token;
   const int lb = blockIdx.x - t * A.wgs_per_token;
   KMOE_MARK(0, 0);
-  uint32_t xr[CPL][16];
+  // the lane's activation chunks as stored: 16 words per chunk (fp16, bf16) or 32 (fp32); XS
+  // instantiates the scaled (bf16 / fp32) form, the fp16 form keeps none of its work
+  const int xdt = XS ? A.xdt : XDT_F16;
+  const bool has_lo = XS && xdt == XDT_F32;
+  const int eb = has_lo ? 4 : 2;
+  const char* const xrow = static_cast<const char*>(A.x) + (size_t)t * H * eb;
+  uint32_t xw[CPL][32];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = lane + 64 * j;
-    if (c < nch) {
-      load16(A.x + (size_t)t * H + (size_t)c * CHUNK, xr[j]);
-    } else {
 #pragma unroll
-      for (int m = 0; m < 16; ++m) xr[j][m] = 0u;
+    for (int m = 0; m < 32; ++m) xw[j][m] = 0u;
+    if (c < nch) {
+      const uint4* q = reinterpret_cast<const uint4*>(xrow + (size_t)c * CHUNK * eb);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = q[i];
+        xw[j][4 * i] = v.x;
+        xw[j][4 * i + 1] = v.y;
+        xw[j][4 * i + 2] = v.z;
+        xw[j][4 * i + 3] = v.w;
+      }
+      if (has_lo) {
+#pragma unroll
+        for (int i = 4; i < 8; ++i) {
+          const uint4 v = q[i];
+          xw[j][4 * i] = v.x;
+          xw[j][4 * i + 1] = v.y;
+          xw[j][4 * i + 2] = v.z;
+          xw[j][4 * i + 3] = v.w;
+        }
+      }
     }
   }
   int my = -1;
@@ -162,7 +195,42 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
     }
   }
   KMOE_MARK(0, 1);
-  uint32_t xp[CPL][16];
+  // fp16 planes of the activations: as loaded (fp16), or scaled per token (bf16, fp32)
+  uint32_t xr[CPL][16], xq[CPL][16];
+  float xinv = 1.f, asc = 1.f;  // 2^-s, and 2^2s for act
+  if (!XS) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        xr[j][m] = xw[j][m];
+        xq[j][m] = 0u;
+      }
+  } else {
+    float v[CPL][32];
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      if (has_lo) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[j][i] = __uint_as_float(xw[j][i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          v[j][2 * i] = __uint_as_float(xw[j][i] << 16);
+          v[j][2 * i + 1] = __uint_as_float(xw[j][i] & 0xFFFF0000u);
+        }
+      }
+      amax = fmaxf(amax, chunk_amax(v[j]));
+    }
+    const int sx = row_scale_exp(__uint_as_float(wave_max_u32_dpp(__float_as_uint(amax))));
+    xinv = exp2i(-sx);
+    asc = exp2i(2 * sx);
+    if (lb == 0 && tid == 0 && A.xinv) A.xinv[t] = xinv;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) split_chunk(v[j], exp2i(sx), xr[j], xq[j]);
+  }
+  uint32_t xp[CPL][16], xlp[CPL][16];
   float xs[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -170,6 +238,16 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
     float sm = 0.f;
 #pragma unroll
     for (int m = 0; m < 16; ++m) sm = fdot2(xr[j][m], ONE2, sm);
+    if (has_lo) {
+      to_pair_order<BITS>(xq[j], xlp[j]);
+      float sl = 0.f;
+#pragma unroll
+      for (int m = 0; m < 16; ++m) sl = fdot2(xq[j][m], ONE2, sl);
+      sm += sl;
+    } else {
+#pragma unroll
+      for (int m = 0; m < 16; ++m) xlp[j][m] = 0u;
+    }
     xs[j] = sm;
     // keep this work ahead of the barrier: sunk into the item loop it would wait behind the
     // first item's weight loads
@@ -276,10 +354,13 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
           uint32_t cg[16], cu[16];
           unpack_chunk<BITS, false>(W.gd[q][r], cg);
           unpack_chunk<BITS, false>(W.ud[q][r], cu);
-          acc[r] += scale_to_f32<BF16>(W.gsc[q][r]) * TWO24 * chunk_dot(cg, xp[q]) +
-                    scale_to_f32<BF16>(W.gbi[q][r]) * xs[q];
-          acc[RW + r] += scale_to_f32<BF16>(W.usc[q][r]) * TWO24 * chunk_dot(cu, xp[q]) +
-                         scale_to_f32<BF16>(W.ubi[q][r]) * xs[q];
+          float dg = chunk_dot(cg, xp[q]), du = chunk_dot(cu, xp[q]);
+          if (has_lo) {
+            dg += chunk_dot(cg, xlp[q]);
+            du += chunk_dot(cu, xlp[q]);
+          }
+          acc[r] += fmaf(scale_to_f32<BF16>(W.gsc[q][r]) * TWO24, dg, scale_to_f32<BF16>(W.gbi[q][r]) * xs[q]);
+          acc[RW + r] += fmaf(scale_to_f32<BF16>(W.usc[q][r]) * TWO24, du, scale_to_f32<BF16>(W.ubi[q][r]) * xs[q]);
         }
       }
     }
@@ -289,7 +370,7 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
     const float uu =
         __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(g), __float_as_uint(g), false, false)[1]);
     if (store_lane) {
-      const float a = activate<ACT>(g, uu);
+      const float a = activate<ACT>(g * xinv, uu * xinv) * asc;
       const _Float16 hi = (_Float16)a;
       const _Float16 lo = (_Float16)(a - (float)hi);
       for (uint64_t m = amask; m; m &= m - 1ull) {  // every assignment of this expert (repeats are rare)
@@ -328,7 +409,8 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int 
                                                          const float* __restrict__ wts,
                                                          const uint16_t* __restrict__ act, size_t act_plane,
                                                          void* __restrict__ out, int out32,
-                                                         const float* __restrict__ shared_out, int lpa_log2, int TG) {
+                                                         const float* __restrict__ shared_out, int lpa_log2, int TG,
+                                                         const float* __restrict__ xinv) {
   __shared__ float red[DEC_STAGE2_ASSIGN * S2_ROWS];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // Token group blockIdx.y: tokens [t0, t0 + TG) are handled as a call of their own, so a
@@ -339,6 +421,7 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int 
     idx += t0 * K;
     if (COMBINE) wts += t0 * K;
     act += (size_t)t0 * K * L.I;
+    if (xinv) xinv += t0;
     if (COMBINE) {
       out = out32 ? static_cast<void*>(static_cast<float*>(out) + (size_t)t0 * L.H)
                   : static_cast<void*>(static_cast<uint16_t*>(out) + (size_t)t0 * L.H);
@@ -426,13 +509,14 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int 
           uint32_t cp[16];
           unpack_chunk<BITS, false>(S.d[r], cp);
           const float sf = scale_to_f32<BF16>(S.sc[r]) * TWO24, bf = scale_to_f32<BF16>(S.bi[r]);
-          part[r] = sf * (chunk_dot(cp, S.xh) + chunk_dot(cp, S.xl)) + bf * xs;
+          part[r] = fmaf(sf, chunk_dot(cp, S.xh) + chunk_dot(cp, S.xl), bf * xs);
         }
       }
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
-        const float v = group_sum_last(part[r], LPA);  // 0 for an assignment with an invalid expert
+        float v = group_sum_last(part[r], LPA);  // 0 for an assignment with an invalid expert
         if (cl == LPA - 1 && u < nunits && U.a < TK) {
+          if (xinv) v *= xinv[U.a / K] * xinv[U.a / K];  // act was stored times 2^2s
           if constexpr (COMBINE) {
             red[U.a * S2_ROWS + (U.hb - h0) + r] = v;
           } else {
@@ -513,7 +597,7 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int 
               uint32_t cp[16];
               unpack_chunk<BITS, false>(d[i][r], cp);
               const float sf = scale_to_f32<BF16>(sc[i][r]) * TWO24, bf = scale_to_f32<BF16>(bi[i][r]);
-              part[i][r] += sf * (chunk_dot(cp, xh[i]) + chunk_dot(cp, xl[i])) + bf * xs;
+              part[i][r] += fmaf(sf, chunk_dot(cp, xh[i]) + chunk_dot(cp, xl[i]), bf * xs);
             }
           }
         }
@@ -523,8 +607,9 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int 
         const int a = av[i];
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-          const float v = group_sum_last(part[i][r], LPA);  // 0 for an assignment with an invalid expert
+          float v = group_sum_last(part[i][r], LPA);  // 0 for an assignment with an invalid expert
           if (cl == LPA - 1 && u0 + 4 * i < nunits && a < TK) {
+            if (xinv) v *= xinv[a / K] * xinv[a / K];  // act was stored times 2^2s
             if constexpr (COMBINE) {
               red[a * S2_ROWS + (hb[i] - h0) + r] = v;
             } else {
@@ -548,7 +633,7 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int 
       float v = 0.f;
       for (int k = 0; k < K; ++k) {
         const int a = t * K + k;
-        v += s_wt[a] * red[a * S2_ROWS + r];
+        v = fmaf(s_wt[a], red[a * S2_ROWS + r], v);
       }
       const int h = h0 + r;
       if (shared_out) v += shared_out[(size_t)t * H + h];
@@ -633,6 +718,7 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   Stage1Args A;
   A.L = L;
   A.x = d.x;
+  A.xdt = d.xdt;
   A.logits = d.logits;
   A.idx_in = d.idx_in;
   A.T = T;
@@ -642,18 +728,22 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   A.scalars = w.scalars;
   A.act = w.act;
   A.act_plane = (size_t)T * K * L.I;
+  A.xinv = d.xdt == XDT_F16 ? nullptr : w.xinv;
   A.wgs_per_expert = L.I / (4 * RW);
   // at most two workgroups per CU in all: every workgroup repeats its token's routing, so the
   // grid stays resident and loops over the token's (expert, row block) items instead
   A.wgs_per_token = max(1, min(min(K, L.E) * A.wgs_per_expert, 2 * cu_count() / T));
   const int grid1 = T * A.wgs_per_token;
   hipError_t err;
-  if (nch <= 64)
-    err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true>, grid1, s, A)
-                   : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false>, grid1, s, A);
-  else
-    err = d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true>, grid1, s, A)
-                   : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false>, grid1, s, A);
+  auto stage1 = [&](auto xs) {
+    constexpr bool XSV = decltype(xs)::value;
+    if (nch <= 64)
+      return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, XSV>, grid1, s, A)
+                      : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, XSV>, grid1, s, A);
+    return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, XSV>, grid1, s, A)
+                    : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, XSV>, grid1, s, A);
+  };
+  err = d.xdt == XDT_F16 ? stage1(std::false_type{}) : stage1(std::true_type{});
   if (err != hipSuccess) return err;
   const int l2 = lpa_log2_for(L.I);
   // Output rows per workgroup (S2_ROWS) and per lane (RPW), and tokens per workgroup (TG).  Every
@@ -669,11 +759,11 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
     const dim3 grid2(L.H / SR, (T + TG - 1) / TG);
     if (d.combine) {
       KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, true>), grid2, dim3(256), 0, s, L,
-                  T, K, idx, d.wts, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, l2, TG);
+                  T, K, idx, d.wts, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, l2, TG, A.xinv);
     } else {
       KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, false>), grid2, dim3(256), 0, s,
                   L, T, K, idx, (const float*)nullptr, (const uint16_t*)w.act, A.act_plane, d.out, 0,
-                  (const float*)nullptr, l2, TG);
+                  (const float*)nullptr, l2, TG, A.xinv);
     }
   };
   using I4 = std::integral_constant<int, 4>;

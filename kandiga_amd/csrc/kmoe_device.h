@@ -247,7 +247,7 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t v) {
 // Dequantize a magic pair word (each half 0x6400|q) to fp16 weights round(q*s + b).
 __device__ __forceinline__ uint32_t dequant_pair(uint32_t magic_pair, half2_t s2, half2_t b2) {
   const half2_t q = __builtin_bit_cast(half2_t, magic_pair) - (half2_t){(_Float16)1024.0f, (_Float16)1024.0f};
-  return __builtin_bit_cast(uint32_t, q * s2 + b2);
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, b2));  // one rounding: round(q*s + b)
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -378,6 +378,70 @@ __device__ __forceinline__ void buf_chunk_cached(__amdgpu_buffer_rsrc_t r, uint3
   } else {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
     d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+  }
+}
+
+// ---- scaled activations (bf16 and fp32 rows) ---------------------------------------------
+// A bf16 or fp32 activation row is taken as fp16 planes of x * 2^s: hi = fp16(x 2^s), and for
+// fp32 rows lo = fp16(x 2^s - hi) (hi + lo carries ~22 bits).  s = 0 when the row's largest
+// magnitude m lies in [2^-4, 2^4) (the rows a normalised model feeds the layer); otherwise 2^s is
+// the power of two that puts m in [1, 2).  Every bf16 element of magnitude at least 2^-14 m is
+// then exact in hi (8 mantissa bits inside fp16's 11, no overflow) and smaller ones keep 2^-24 m
+// absolute precision, so bf16's whole range is usable.  The gate/up products are taken on the
+// scaled row and multiplied by 2^-s in fp32 (exact); the SwiGLU output, which grows with the
+// square of the row, is stored times 2^2s, and the down projection's result is multiplied by
+// 2^-2s, so the fp16 act planes stay in range for rows far outside fp16's.  With s = 0 the
+// arithmetic is the fp16 path's, so fp16-representable rows in that window give its results bit
+// for bit.  A row that is all zero or holds an infinity keeps s = 0 (non-finite values propagate).
+
+// s for a row whose largest magnitude is amax (NaN elements do not take part).
+__device__ __forceinline__ int row_scale_exp(float amax) {
+  if (!(amax > 0.f) || !__builtin_isfinite(amax)) return 0;
+  const int e = (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127;  // floor(log2 amax) (normal amax)
+  if (e >= -4 && e < 4) return 0;
+  return min(60, max(-60, -e));
+}
+__device__ __forceinline__ float exp2i(int s) { return __uint_as_float((uint32_t)(127 + s) << 23); }
+
+// 32 consecutive activations of a bf16 (xdt 1) or fp32 (xdt 2) row, as fp32.
+__device__ __forceinline__ void load_chunk_vals(const void* p, int xdt, float (&v)[32]) {
+  if (xdt == 1) {
+    uint32_t w[16];
+    load16g(p, w);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  } else {
+    const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 t = q[i];
+      v[4 * i] = t.x;
+      v[4 * i + 1] = t.y;
+      v[4 * i + 2] = t.z;
+      v[4 * i + 3] = t.w;
+    }
+  }
+}
+
+__device__ __forceinline__ float chunk_amax(const float (&v)[32]) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
+  return m;
+}
+
+// hi and lo planes of v * k as fp16 pairs in natural order (element 2i low, 2i+1 high).
+__device__ __forceinline__ void split_chunk(const float (&v)[32], float k, uint32_t (&hi)[16], uint32_t (&lo)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float a = v[2 * i] * k, b = v[2 * i + 1] * k;
+    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    const _Float16 la = (_Float16)(a - (float)ha), lb = (_Float16)(b - (float)hb);
+    hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+    lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, la) | ((uint32_t)__builtin_bit_cast(uint16_t, lb) << 16);
   }
 }
 
@@ -546,6 +610,50 @@ __device__ __forceinline__ int block_prefix_count(bool flag, int32_t* tmp, int* 
   __syncthreads();
   *total = tot;
   return before;
+}
+
+// One wave writes token t's activations into the grouped GEMM's A layout: xpp row t in pair
+// order (per 32-wide chunk).  fp16 rows (xdt 0) are permuted as they are; bf16 (1) and fp32 (2)
+// rows are scaled (see the scaled activations above: xinv[t] = 2^-s), the hi plane going to xpp
+// and, for fp32, the lo plane to xpp + plane.  Two passes over the row for bf16/fp32 (the largest
+// magnitude first, the second pass mostly from L2).
+template <int BITS>
+__device__ __forceinline__ void token_to_pairs(const void* x, int xdt, int t, int H, int lane, uint16_t* xpp,
+                                               size_t plane, float* xinv) {
+  const int nch = H / CHUNK;
+  if (xdt == 0) {
+    const uint16_t* xr = static_cast<const uint16_t*>(x) + (size_t)t * H;
+    for (int c = lane; c < nch; c += 64) {
+      uint32_t nat[16], pr[16];
+      load16g(xr + c * CHUNK, nat);
+      to_pair_order<BITS>(nat, pr);
+      store16s(reinterpret_cast<_Float16*>(xpp + (size_t)t * H + c * CHUNK), pr);
+    }
+    return;
+  }
+  const int eb = xdt == 2 ? 4 : 2;
+  const char* xr = static_cast<const char*>(x) + (size_t)t * H * eb;
+  float amax = 0.f;
+  for (int c = lane; c < nch; c += 64) {
+    float v[32];
+    load_chunk_vals(xr + (size_t)c * CHUNK * eb, xdt, v);
+    amax = fmaxf(amax, chunk_amax(v));
+  }
+  const int sx = row_scale_exp(__uint_as_float(wave_max_u32_dpp(__float_as_uint(amax))));
+  if (lane == 0) xinv[t] = exp2i(-sx);
+  const float k = exp2i(sx);
+  for (int c = lane; c < nch; c += 64) {
+    float v[32];
+    uint32_t hi[16], lo[16], pr[16];
+    load_chunk_vals(xr + (size_t)c * CHUNK * eb, xdt, v);
+    split_chunk(v, k, hi, lo);
+    to_pair_order<BITS>(hi, pr);
+    store16s(reinterpret_cast<_Float16*>(xpp + (size_t)t * H + c * CHUNK), pr);
+    if (xdt == 2) {
+      to_pair_order<BITS>(lo, pr);
+      store16s(reinterpret_cast<_Float16*>(xpp + plane + (size_t)t * H + c * CHUNK), pr);
+    }
+  }
 }
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }

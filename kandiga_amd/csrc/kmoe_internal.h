@@ -69,7 +69,9 @@ struct Work {
   uint16_t* act;       // 2 planes [T*K][I] fp16 (hi, lo), pair order; rows by assignment
                        // (decode) or by expert-sorted position (grouped GEMM)
   float* y32;          // [T*K][H] fp32 weighted per-assignment outputs (grouped-GEMM path of forward)
-  uint16_t* xpp;       // [T][H] x in pair order (grouped-GEMM path)
+  uint16_t* xpp;       // x in pair order (grouped-GEMM path): hi plane [T][H], then the lo plane
+                       // (fp32 activations)
+  float* xinv;         // [T] 2^-s of each token's activation scaling (bf16 / fp32 activations)
   float* shared_out;     // [T][H] fp32 dense shared-expert output
   uint16_t* shared_act;  // shared-expert SwiGLU output: 2 fp16 planes [T][Is] (decode) or 1 (prefill)
 };
@@ -84,9 +86,13 @@ constexpr int DEC_STAGE2_ASSIGN = 128; // assignments held in two lane slots by 
 // Device error flag bits (Work::scalars[2]).
 constexpr int DEVERR_BAD_EXPERT = 1;
 
+// Activation dtypes of the C ABI (KMOE_X_*): rows [T][H] of fp16, bf16 or fp32.  bf16 and fp32
+// rows are taken per token as fp16 planes of x * 2^s (kmoe_device.h, scaled activations).
+constexpr int XDT_F16 = 0, XDT_BF16 = 1, XDT_F32 = 2;
+
 // One decode-path call (1..DEC_MAX_TOKENS tokens): routing from logits, or given indices.
 struct DecodeCall {
-  const uint16_t* x;       // [T][H]
+  const void* x;           // [T][H] of dtype xdt
   const float* logits;     // [T][E], or null when idx_in is given
   const int32_t* idx_in;   // [T][K], or null when routing
   int T;
@@ -99,6 +105,7 @@ struct DecodeCall {
   bool combine;
   const float* extra;      // [T][H] fp32 added after the combine (block residual + gated shared
                            // expert), or null: then the layer's dense shared expert output, if any
+  int xdt;                 // XDT_* of x
 };
 
 // Kernel timing hook (kmoe_profile_begin/end).  prof_events hands out the next event pair of
@@ -127,7 +134,7 @@ namespace kmoe {
 // those of kmoe_forward.
 int forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                  int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
-                 void* stream, const float* extra = nullptr);
+                 void* stream, const float* extra = nullptr, int xdt = XDT_F16);
 // kmoe_workspace_size for `tokens` tokens of `layer`.
 int workspace_bytes_for(const kmoe_layer* layer, int32_t tokens, size_t* bytes);
 // Records `msg` as the calling thread's last error and returns `code`.
@@ -135,23 +142,29 @@ int report_error(int code, const char* msg);
 
 // ---- launchers (return hipError_t of the launch) ----------------------------------------
 hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, float* wts, hipStream_t s);
-// launch_route plus xpp = x [T][H] in pair order for `bits`-bit codes (one launch).
-hipError_t launch_route_xpair(const float* logits, int T, int E, int K, int32_t* idx, float* wts, const uint16_t* x,
-                              int H, int bits, uint16_t* xpp, hipStream_t s);
+// launch_route plus xpp = x [T][H] in pair order for `bits`-bit codes (one launch); bf16 / fp32
+// rows go in scaled (xinv[t] = 2^-s), fp32 rows as two planes (lo plane at xpp + T*H).
+hipError_t launch_route_xpair(const float* logits, int T, int E, int K, int32_t* idx, float* wts, const void* x,
+                              int xdt, int H, int bits, uint16_t* xpp, float* xinv, hipStream_t s);
 // bm: rows per grouped-GEMM tile of the m-tile list (GEMM_BM, or GEMM_BM_PACK for a layer with
 // the prefill copy; launch_gemm must be called for the same layer).
 hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& w, int max_mtiles, int bm,
                           hipStream_t s);
 // Tiles of 64 rows pay off with the prefill copy's cheap weight loads, up to a gate/up k loop of
 // 2048; past that the 128-row tile's weight reuse wins.
-inline int gemm_bm(const LayerArgs& a) { return a.pk[0].codes && a.H <= 2048 ? GEMM_BM_PACK : GEMM_BM; }
+// fp32 activations (two A planes in the gate/up GEMM) always use 128-row tiles.
+inline int gemm_bm(const LayerArgs& a, int xdt = XDT_F16) {
+  return a.pk[0].codes && a.H <= 2048 && xdt != XDT_F32 ? GEMM_BM_PACK : GEMM_BM;
+}
 hipError_t launch_decode(const LayerConfig& c, const DecodeCall& d, hipStream_t s);
-// x [T][H] -> xpp in pair order (per 32-wide chunk), the gate/up GEMM's A layout.
-hipError_t launch_xpair(const LayerConfig& c, const uint16_t* x, int T, uint16_t* xpp, hipStream_t s);
+// x [T][H] -> xpp in pair order (per 32-wide chunk), the gate/up GEMM's A layout (bf16 / fp32
+// rows scaled and split as for launch_route_xpair).
+hipError_t launch_xpair(const LayerConfig& c, const void* x, int xdt, int T, uint16_t* xpp, float* xinv, hipStream_t s);
 // Per-assignment outputs: y16 (fp16, unweighted: the switch_mlp contract) or, when y16 is
 // null, Work::y32 (fp32, each row scaled by its routing weight in wscale for the combine).
 hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Work& w, int max_mtiles,
-                       uint16_t* y16, const float* wscale, hipStream_t s);
+                       uint16_t* y16, const float* wscale, hipStream_t s, int xdt = XDT_F16,
+                       const float* xinv = nullptr);
 // y[a] (fp16 [TK][H]) = 0 for every assignment a whose idx[a] lies outside [0, E).
 hipError_t launch_zero_bad_rows(const int32_t* idx, int TK, int E, int H, uint16_t* y, hipStream_t s);
 // out[t] = sum_k (wts ? wts[t,k] : 1) * y[t,k] (+ shared[t]); y is fp32 (y32) or fp16 bits (y16).

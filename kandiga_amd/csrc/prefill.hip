@@ -124,11 +124,12 @@ __global__ __launch_bounds__(256) void xpair_kernel(const uint16_t* __restrict__
 constexpr int LDA = 72;                      // halves per row of the A slab (64 + 8 pad: 144 B)
 constexpr int EPI_LD = 68;                   // floats per row of a wave's down epilogue staging (64 + 4)
 constexpr int EPA_LD = 40;                   // halves per row of a wave's gate/up epilogue staging (32 + 8)
-// LDS of a GEMM workgroup in halves: two stages of A slabs (one plane for gate/up, the hi and
-// lo planes for down), or the epilogue staging if larger
-constexpr int lds_halves(int bm, bool down) {
-  return (down ? 4 : 2) * bm * LDA > (down ? 4 * 32 * EPI_LD * 2 : 4 * 32 * EPA_LD)
-             ? (down ? 4 : 2) * bm * LDA
+// LDS of a GEMM workgroup in halves: two stages of A slabs (np planes for gate/up: one, or the hi
+// and lo planes of fp32 activations; the hi and lo planes of act for down), or the epilogue
+// staging if larger
+constexpr int lds_halves(int bm, bool down, int np = 1) {
+  return 2 * (down ? 2 : np) * bm * LDA > (down ? 4 * 32 * EPI_LD * 2 : 4 * 32 * EPA_LD)
+             ? 2 * (down ? 2 : np) * bm * LDA
              : (down ? 4 * 32 * EPI_LD * 2 : 4 * 32 * EPA_LD);
 }
 
@@ -379,11 +380,15 @@ constexpr int DN_COLS = 4 * 64;  // output columns per down workgroup
 // gate/up GEMM + SwiGLU.  Column tile ct covers intermediate columns [128ct, 128ct + 128); wave w
 // the 32 columns c0 = 128ct + 32w + n.  Each lane holds matching gate and up values and writes
 // act = silu(gate) * up (fp16, pair order within each 32-column chunk, the down projection's k
-// order) for the sorted position of each row.
-template <int BITS, bool BF16, int ACT, int NB, int BL, int BM>
-__device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* __restrict__ x, int K,
-                                            const int32_t* __restrict__ perm, int e, int row0, int nrows, int ct,
-                                            _Float16* sA, uint16_t* __restrict__ act, size_t plane) {
+// order) for the sorted position of each row.  Scaled activations (bf16 / fp32 rows): s_xs[r]
+// holds 2^-s of row r's token, applied to gate and up before the activation, and act is stored
+// times 2^2s (the down GEMM takes it back); NPX = 2 multiplies each weight fragment by the hi
+// and the lo plane of fp32 rows (lo plane at x + xplane).
+template <int BITS, bool BF16, int ACT, int NB, int BL, int BM, int NPX>
+__device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* __restrict__ x, size_t xplane,
+                                            int K, const int32_t* __restrict__ perm, int e, int row0, int nrows,
+                                            int ct, _Float16* sA, const float* s_xs, uint16_t* __restrict__ act,
+                                            size_t plane) {
   const int H = L.H, I = L.I;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
   const int lr = tid / (256 / BM);
@@ -419,7 +424,7 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
   }
   float16_t acc[4][2];
   zero_acc(acc);
-  gemm_mainloop<BITS, BF16, NB, 2, BL, BM, 1>(acc, sA, x + (size_t)tok * H, 0, R, (int)ng);
+  gemm_mainloop<BITS, BF16, NB, 2, BL, BM, NPX>(acc, sA, x + (size_t)tok * H, xplane, R, (int)ng);
   // Epilogue through LDS (the slabs are free once every wave is past the k loop): per 32-row
   // block and plane (hi, then lo) the wave writes its 32 x 32 act values at their pair-order
   // columns, then each lane stores 8 consecutive columns (16 bytes) of a row.
@@ -429,8 +434,16 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
 #pragma unroll
   for (int mb = 0; mb < NB; ++mb) {
     float a[16];
+    if (s_xs) {  // gate and up times 2^-s; act stored times 2^2s
 #pragma unroll
-    for (int v = 0; v < 16; ++v) a[v] = activate_p<ACT>(acc[mb][0][v], acc[mb][1][v]);
+      for (int v = 0; v < 16; ++v) {
+        const float xs = s_xs[32 * mb + 8 * (v >> 2) + 4 * h + (v & 3)];
+        a[v] = activate_p<ACT>(acc[mb][0][v] * xs, acc[mb][1][v] * xs) * (1.0f / (xs * xs));
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) a[v] = activate_p<ACT>(acc[mb][0][v], acc[mb][1][v]);
+    }
 #pragma unroll
     for (int pl = 0; pl < 2; ++pl) {
 #pragma unroll
@@ -453,29 +466,38 @@ __device__ __forceinline__ void gateup_tile(const LayerArgs& L, const uint16_t* 
 
 // BM rows per tile: 128, or 64 where the shorter tile's 64 accumulators let three gate/up or
 // (down_wgs) up to four down workgroups share a CU.
-template <int BITS, bool BF16, int ACT, int BL, int BM>
+template <int BITS, bool BF16, int ACT, int BL, int BM, int NPX>
 __global__ __launch_bounds__(256, BM == 64 ? 3 : 2) void gemm_gateup_kernel(const LayerArgs L, const uint16_t* __restrict__ x,
+                                                             size_t xplane, const float* __restrict__ xinv,
                                                              int K, const int32_t* __restrict__ perm,
                                                              const int32_t* __restrict__ scalars,
                                                              const int32_t* __restrict__ mt_expert,
                                                              const int32_t* __restrict__ mt_row0,
                                                              const int32_t* __restrict__ mt_rows,
                                                              uint16_t* __restrict__ act, size_t plane) {
-  __shared__ __attribute__((aligned(16))) _Float16 sA[lds_halves(BM, false)];
+  __shared__ __attribute__((aligned(16))) _Float16 sA[lds_halves(BM, false, NPX)];
+  __shared__ float s_xs[BM];
   int mt, ct;
   if (!xcd_mtile(blockIdx.x, (L.I + GU_COLS - 1) / GU_COLS, uniform(scalars[1]), mt, ct)) return;
   const int e = uniform(mt_expert[mt]), row0 = uniform(mt_row0[mt]), nrows = uniform(mt_rows[mt]);
+  // per-row 2^-s of scaled activations (written before the k loop's first barrier)
+  if (xinv) {
+    for (int r = threadIdx.x; r < BM; r += 256) s_xs[r] = xinv[perm[row0 + min(r, nrows - 1)] / K];
+  }
+  const float* xs = xinv ? s_xs : nullptr;
+#define KMOE_GUT(NBV) gateup_tile<BITS, BF16, ACT, NBV, BL, BM, NPX>(L, x, xplane, K, perm, e, row0, nrows, ct, sA, xs, act, plane)
   if constexpr (BM == 64) {
-    if (nrows <= 32) gateup_tile<BITS, BF16, ACT, 1, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane);
-    else gateup_tile<BITS, BF16, ACT, 2, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane);
+    if (nrows <= 32) KMOE_GUT(1);
+    else KMOE_GUT(2);
   } else {
     switch ((nrows + 31) >> 5) {
-      case 1: gateup_tile<BITS, BF16, ACT, 1, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane); break;
-      case 2: gateup_tile<BITS, BF16, ACT, 2, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane); break;
-      case 3: gateup_tile<BITS, BF16, ACT, 3, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane); break;
-      default: gateup_tile<BITS, BF16, ACT, 4, BL, BM>(L, x, K, perm, e, row0, nrows, ct, sA, act, plane); break;
+      case 1: KMOE_GUT(1); break;
+      case 2: KMOE_GUT(2); break;
+      case 3: KMOE_GUT(3); break;
+      default: KMOE_GUT(4); break;
     }
   }
+#undef KMOE_GUT
 }
 
 // down GEMM.  Column tile ct covers output columns [256ct, 256ct + 256); wave w the 64 columns
@@ -578,10 +600,11 @@ __global__ __launch_bounds__(256, down_wgs(BITS, BF16, BM)) void gemm_down_kerne
                                                            const int32_t* __restrict__ mt_rows,
                                                            const uint16_t* __restrict__ act, size_t plane,
                                                            const float* __restrict__ wscale,
-                                                           float* __restrict__ y32, uint16_t* __restrict__ y16) {
+                                                           float* __restrict__ y32, uint16_t* __restrict__ y16,
+                                                           const float* __restrict__ xinv, int K) {
   __shared__ __attribute__((aligned(16))) _Float16 sA[lds_halves(BM, true)];
-  __shared__ int32_t s_asg[BM];  // assignment of each tile row, and its routing weight
-  __shared__ float s_wa[BM];
+  __shared__ int32_t s_asg[BM];  // assignment of each tile row, and its output scale: the routing
+  __shared__ float s_wa[BM];     // weight, times 2^-2s of scaled activations
   int mt, ct;
   if (!xcd_mtile(blockIdx.x, (L.H + DN_COLS - 1) / DN_COLS, uniform(scalars[1]), mt, ct)) return;
   const int e = uniform(mt_expert[mt]), row0 = uniform(mt_row0[mt]), nrows = uniform(mt_rows[mt]);
@@ -589,7 +612,9 @@ __global__ __launch_bounds__(256, down_wgs(BITS, BF16, BM)) void gemm_down_kerne
   if (tid < BM) {  // read after the k loop's barriers
     const int a = tid < nrows ? perm[row0 + tid] : 0;
     s_asg[tid] = a;
-    s_wa[tid] = wscale && tid < nrows ? wscale[a] : 1.0f;
+    float wa = wscale && tid < nrows ? wscale[a] : 1.0f;
+    if (xinv) wa *= xinv[a / K] * xinv[a / K];
+    s_wa[tid] = wa;
   }
   if constexpr (BM == 64) {
     if (nrows <= 32) down_tile<BITS, BF16, OUT16, 1, BL, BM>(L, e, row0, nrows, ct, sA, s_asg, s_wa, act, plane, y32, y16);
@@ -646,7 +671,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const Y* __restrict__ y, c
 // ---- launchers --------------------------------------------------------------------------
 template <int BITS, bool BF16, int ACT>
 static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, const Work& w, int max_mtiles,
-                            uint16_t* y16, const float* wscale, hipStream_t s) {
+                            uint16_t* y16, const float* wscale, hipStream_t s, int xdt, const float* xinv) {
   const LayerArgs& L = c.args;
   const size_t plane = (size_t)T * c.top_k * L.I;  // act lo plane offset (the workspace holds both planes)
   const int per_xcd = (max_mtiles + 7) / 8;  // m-tiles of one XCD's share at most (see xcd_mtile)
@@ -654,15 +679,18 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
   // weights from the prefill copy when the layer has one, else the MLX tensors with scales in
   // pairs of groups when the rows hold an even number of groups
   const bool pk = L.pk[0].codes != nullptr;
-  const int bm = gemm_bm(L);  // the m-tile list was built with this many rows per tile
+  const int bm = gemm_bm(L, xdt);  // the m-tile list was built with this many rows per tile
+  const size_t xplane = (size_t)T * L.H;  // lo plane of fp32 activations
   const int bl_gu = pk ? 2 : (L.H / GROUP) % 2 == 0 ? 1 : 0;
   const int bl_dn = pk ? 2 : (L.I / GROUP) % 2 == 0 ? 1 : 0;
-#define KMOE_GU(BLV, BMV)                                                                                    \
-  KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, BLV, BMV>), grid_gu, dim3(256), 0, s, L, \
-              x, c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act, plane)
-  if (bl_gu == 2) {
-    if (bm == 64) KMOE_GU(2, 64); else KMOE_GU(2, 128);
-  } else if (bl_gu == 1) KMOE_GU(1, 128); else KMOE_GU(0, 128);
+#define KMOE_GU(BLV, BMV, NPXV)                                                                                \
+  KMOE_LAUNCH("gemm_gateup_kernel", (gemm_gateup_kernel<BITS, BF16, ACT, BLV, BMV, NPXV>), grid_gu, dim3(256), 0, s, \
+              L, x, xplane, xinv, c.top_k, w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, w.act, plane)
+  if (xdt == XDT_F32) {  // two activation planes, 128-row tiles
+    if (bl_gu == 2) KMOE_GU(2, 128, 2); else if (bl_gu == 1) KMOE_GU(1, 128, 2); else KMOE_GU(0, 128, 2);
+  } else if (bl_gu == 2) {
+    if (bm == 64) KMOE_GU(2, 64, 1); else KMOE_GU(2, 128, 1);
+  } else if (bl_gu == 1) KMOE_GU(1, 128, 1); else KMOE_GU(0, 128, 1);
 #undef KMOE_GU
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
@@ -670,7 +698,7 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
 #define KMOE_DOWN(OUT16, BLV, BMV)                                                                              \
   KMOE_LAUNCH("gemm_down_kernel", (gemm_down_kernel<BITS, BF16, OUT16, BLV, BMV>), grid_dn, dim3(256), 0, s, L,   \
               w.perm, w.scalars, w.mt_expert, w.mt_row0, w.mt_rows, (const uint16_t*)w.act, plane, wscale,      \
-              OUT16 ? (float*)nullptr : w.y32, OUT16 ? y16 : (uint16_t*)nullptr)
+              OUT16 ? (float*)nullptr : w.y32, OUT16 ? y16 : (uint16_t*)nullptr, xinv, c.top_k)
   if (y16) {
     if (bl_dn == 2) {
       if (bm == 64) KMOE_DOWN(true, 2, 64); else KMOE_DOWN(true, 2, 128);
@@ -685,16 +713,16 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
 }
 
 hipError_t launch_gemm(const LayerConfig& c, const uint16_t* x, int T, const Work& w, int max_mtiles, uint16_t* y16,
-                       const float* wscale, hipStream_t s) {
+                       const float* wscale, hipStream_t s, int xdt, const float* xinv) {
   if (max_mtiles == 0) return hipSuccess;
+#define KMOE_GI(B, F, A) gemm_impl<B, F, A>(c, x, T, w, max_mtiles, y16, wscale, s, xdt, xinv)
   if (c.bits == 3) {
-    if (c.bf16_scales)
-      return c.act ? gemm_impl<3, true, 1>(c, x, T, w, max_mtiles, y16, wscale, s) : gemm_impl<3, true, 0>(c, x, T, w, max_mtiles, y16, wscale, s);
-    return c.act ? gemm_impl<3, false, 1>(c, x, T, w, max_mtiles, y16, wscale, s) : gemm_impl<3, false, 0>(c, x, T, w, max_mtiles, y16, wscale, s);
+    if (c.bf16_scales) return c.act ? KMOE_GI(3, true, 1) : KMOE_GI(3, true, 0);
+    return c.act ? KMOE_GI(3, false, 1) : KMOE_GI(3, false, 0);
   }
-  if (c.bf16_scales)
-    return c.act ? gemm_impl<4, true, 1>(c, x, T, w, max_mtiles, y16, wscale, s) : gemm_impl<4, true, 0>(c, x, T, w, max_mtiles, y16, wscale, s);
-  return c.act ? gemm_impl<4, false, 1>(c, x, T, w, max_mtiles, y16, wscale, s) : gemm_impl<4, false, 0>(c, x, T, w, max_mtiles, y16, wscale, s);
+  if (c.bf16_scales) return c.act ? KMOE_GI(4, true, 1) : KMOE_GI(4, true, 0);
+  return c.act ? KMOE_GI(4, false, 1) : KMOE_GI(4, false, 0);
+#undef KMOE_GI
 }
 
 // y[a] = 0 for the assignments whose expert index lies outside [0, E).  The permutation drops
@@ -717,14 +745,35 @@ hipError_t launch_zero_bad_rows(const int32_t* idx, int TK, int E, int H, uint16
   return hipGetLastError();
 }
 
-hipError_t launch_xpair(const LayerConfig& c, const uint16_t* x, int T, uint16_t* xpp, hipStream_t s) {
+// One wave per token: bf16 / fp32 activations into the A layout (token_to_pairs).
+template <int BITS>
+__global__ __launch_bounds__(256) void xprep_kernel(const void* __restrict__ x, int xdt, int T, int H,
+                                                    uint16_t* __restrict__ xpp, size_t plane,
+                                                    float* __restrict__ xinv) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  token_to_pairs<BITS>(x, xdt, t, H, threadIdx.x & 63, xpp, plane, xinv);
+}
+
+hipError_t launch_xpair(const LayerConfig& c, const void* x, int xdt, int T, uint16_t* xpp, float* xinv,
+                        hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  if (xdt != XDT_F16) {
+    const dim3 grid((T + 3) / 4);
+    const size_t plane = (size_t)T * c.args.H;
+    if (c.bits == 3)
+      KMOE_LAUNCH("xprep_kernel", xprep_kernel<3>, grid, dim3(256), 0, s, x, xdt, T, c.args.H, xpp, plane, xinv);
+    else
+      KMOE_LAUNCH("xprep_kernel", xprep_kernel<4>, grid, dim3(256), 0, s, x, xdt, T, c.args.H, xpp, plane, xinv);
+    return hipGetLastError();
+  }
   const size_t nchunks = (size_t)T * c.args.H / CHUNK;
-  if (nchunks == 0) return hipSuccess;
   const dim3 grid((unsigned)((nchunks + 255) / 256));
+  const uint16_t* x16 = static_cast<const uint16_t*>(x);
   if (c.bits == 3) {
-    KMOE_LAUNCH("xpair_kernel", xpair_kernel<3>, grid, dim3(256), 0, s, x, nchunks, xpp);
+    KMOE_LAUNCH("xpair_kernel", xpair_kernel<3>, grid, dim3(256), 0, s, x16, nchunks, xpp);
   } else {
-    KMOE_LAUNCH("xpair_kernel", xpair_kernel<4>, grid, dim3(256), 0, s, x, nchunks, xpp);
+    KMOE_LAUNCH("xpair_kernel", xpair_kernel<4>, grid, dim3(256), 0, s, x16, nchunks, xpp);
   }
   return hipGetLastError();
 }

@@ -37,20 +37,16 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 template <int BITS>
 __global__ __launch_bounds__(256) void route_xpair_kernel(const float* __restrict__ logits, int T, int E, int K,
                                                           int32_t* __restrict__ idx, float* __restrict__ wts,
-                                                          const uint16_t* __restrict__ x, int H,
-                                                          uint16_t* __restrict__ xpp) {
+                                                          const void* __restrict__ x, int xdt, int H,
+                                                          uint16_t* __restrict__ xpp, size_t plane,
+                                                          float* __restrict__ xinv) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (t >= T) return;
   const float* row = logits + (size_t)t * E;
   int32_t* io = idx + (size_t)t * K;
   float* wo = wts + (size_t)t * K;
   KMOE_TOPK_DISPATCH(E, (wave_topk<EPL_>(row, E, K, io, wo, nullptr, nullptr)));
-  for (int c = lane; c < H / CHUNK; c += 64) {
-    uint32_t nat[16], pr[16];
-    load16g(x + (size_t)t * H + c * CHUNK, nat);
-    to_pair_order<BITS>(nat, pr);
-    store16s(reinterpret_cast<_Float16*>(xpp + (size_t)t * H + c * CHUNK), pr);
-  }
+  token_to_pairs<BITS>(x, xdt, t, H, lane, xpp, plane, xinv);
 }
 
 __global__ __launch_bounds__(256) void permute_rank_kernel(const int32_t* __restrict__ idx, int TK, int E,
@@ -234,16 +230,17 @@ hipError_t launch_route(const float* logits, int T, int E, int K, int32_t* idx, 
   return hipGetLastError();
 }
 
-hipError_t launch_route_xpair(const float* logits, int T, int E, int K, int32_t* idx, float* wts, const uint16_t* x,
-                              int H, int bits, uint16_t* xpp, hipStream_t s) {
+hipError_t launch_route_xpair(const float* logits, int T, int E, int K, int32_t* idx, float* wts, const void* x,
+                              int xdt, int H, int bits, uint16_t* xpp, float* xinv, hipStream_t s) {
   if (T == 0) return hipSuccess;
   const dim3 grid((T + 3) / 4);
+  const size_t plane = (size_t)T * H;
   if (bits == 3)
-    KMOE_LAUNCH("route_xpair_kernel", route_xpair_kernel<3>, grid, dim3(256), 0, s, logits, T, E, K, idx, wts, x, H,
-                xpp);
+    KMOE_LAUNCH("route_xpair_kernel", route_xpair_kernel<3>, grid, dim3(256), 0, s, logits, T, E, K, idx, wts, x, xdt,
+                H, xpp, plane, xinv);
   else
-    KMOE_LAUNCH("route_xpair_kernel", route_xpair_kernel<4>, grid, dim3(256), 0, s, logits, T, E, K, idx, wts, x, H,
-                xpp);
+    KMOE_LAUNCH("route_xpair_kernel", route_xpair_kernel<4>, grid, dim3(256), 0, s, logits, T, E, K, idx, wts, x, xdt,
+                H, xpp, plane, xinv);
   return hipGetLastError();
 }
 

@@ -310,6 +310,19 @@ def _on_device(t: torch.Tensor, dev: torch.device, name: str) -> None:
         raise ValueError(f"{name} is on {t.device}, the experts are on {dev}")
 
 
+_X_DTYPES = {torch.float16: _capi.X_F16, torch.bfloat16: _capi.X_BF16, torch.float32: _capi.X_F32}
+
+
+def _x_arg(x: torch.Tensor, H: int):
+    """(rows [T, H] contiguous, KMOE_X_* code) for the entry points that take fp16, bf16 or fp32
+    activations natively (kmoe_expert_mlp_x / kmoe_forward_x)."""
+    if x.shape[-1] != H:
+        raise ValueError(f"last dimension of x is {x.shape[-1]}, expected {H}")
+    if x.dtype not in _X_DTYPES:
+        raise TypeError(f"x must be float16, bfloat16 or float32, got {x.dtype}")
+    return x.reshape(-1, H).contiguous(), _X_DTYPES[x.dtype]
+
+
 def _check_x(x: torch.Tensor, H: int) -> torch.Tensor:
     if x.shape[-1] != H:
         raise ValueError(f"last dimension of x is {x.shape[-1]}, expected {H}")
@@ -336,15 +349,15 @@ class QuantizedSwitchGLU:
         K = indices.shape[-1]
         if K != E.shape.top_k:
             raise ValueError(f"indices have {K} experts per token, layer was built for top_k={E.shape.top_k}")
-        xf = _check_x(x, E.shape.hidden)
+        xf, xdt = _x_arg(x, E.shape.hidden)
         idx = indices.reshape(-1, K).to(torch.int32).contiguous()
         T = xf.shape[0]
         if idx.shape[0] != T:
             raise ValueError("x and indices disagree on the number of tokens")
         y = torch.empty((T, K, E.shape.hidden), dtype=torch.float16, device=E.device)
         ws = E.workspace(T)
-        _capi.check(_capi.lib().kmoe_expert_mlp(E._handle, xf.data_ptr(), idx.data_ptr(), T, y.data_ptr(),
-                                                ws.data_ptr(), ws.numel(), _stream()), "kmoe_expert_mlp")
+        _capi.check(_capi.lib().kmoe_expert_mlp_x(E._handle, xf.data_ptr(), xdt, idx.data_ptr(), T, y.data_ptr(),
+                                                  ws.data_ptr(), ws.numel(), _stream()), "kmoe_expert_mlp_x")
         return y.reshape(*indices.shape, E.shape.hidden)
 
 
@@ -361,14 +374,18 @@ class SparseMoeBlock:
 
     def __call__(self, x: torch.Tensor, logits: torch.Tensor, return_routing: bool = False,
                  out_dtype: torch.dtype = torch.float16):
-        """``out_dtype`` float16 (default) or float32 (the combine result before fp16 rounding)."""
+        """``x`` float16, bfloat16 or float32 (taken natively; a layer with the dense fp16 shared
+        expert takes float16 only); ``out_dtype`` float16 (default) or float32 (the combine result
+        before fp16 rounding)."""
         E = self.experts
         if out_dtype not in (torch.float16, torch.float32):
             raise TypeError("out_dtype must be torch.float16 or torch.float32")
         _on_device(x, E.device, "x")
         _on_device(logits, E.device, "logits")
         lead = x.shape[:-1]
-        xf = _check_x(x, E.shape.hidden)
+        xf, xdt = _x_arg(x, E.shape.hidden)
+        if xdt != _capi.X_F16 and E.shared:
+            raise TypeError("a layer with the dense fp16 shared expert takes float16 x only")
         lg = logits.reshape(-1, E.shape.num_experts).to(torch.float32).contiguous()
         T = xf.shape[0]
         if lg.shape[0] != T:
@@ -380,9 +397,9 @@ class SparseMoeBlock:
             w = torch.empty((T, E.shape.top_k), dtype=torch.float32, device=E.device)
         ws = E.workspace(T)
         odt = _capi.OUT_F32 if out_dtype == torch.float32 else _capi.OUT_F16
-        _capi.check(_capi.lib().kmoe_forward(E._handle, xf.data_ptr(), lg.data_ptr(), T, out.data_ptr(), odt,
-                                             _ptr(idx), _ptr(w), ws.data_ptr(), ws.numel(), _stream()),
-                    "kmoe_forward")
+        _capi.check(_capi.lib().kmoe_forward_x(E._handle, xf.data_ptr(), xdt, lg.data_ptr(), T, out.data_ptr(), odt,
+                                               _ptr(idx), _ptr(w), ws.data_ptr(), ws.numel(), _stream()),
+                    "kmoe_forward_x")
         out = out.reshape(*lead, E.shape.hidden)
         if return_routing:
             return out, idx.reshape(*lead, -1), w.reshape(*lead, -1)

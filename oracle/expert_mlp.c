@@ -172,15 +172,15 @@ static void* fan_worker(void* arg) {
     return NULL;
 }
 
-/*
- * switch_mlp contract (kandiga/engine.py:670-739): y[t, k, :] = expert idx[t, k] applied to x[t].
- * x is fp16 [T, H] (converted to fp32 as kandiga_cpu_expert.m:670-674), y is fp32 [T, K, H]
- * (the value bakan_cpu_expert_mlp returns before its fp16 rounding).
- * nthreads <= 1 runs single-threaded; otherwise each token fans its K experts over
- * min(K, nthreads) threads and joins before the next token, as the reference does.
- */
-int oracle_switch_mlp(const oracle_layer* L, const uint16_t* x_f16, const int32_t* idx, int T, int K, float* y,
-                      int nthreads) {
+/* One token row of x as fp32: fp16 bits widened (kandiga_cpu_expert.m:670-674), or fp32 as given
+ * (bakan_cpu_expert_mlp, :471-552; the bf16 entry widens bf16 to fp32 and calls it, :690-719). */
+static void token_row(const uint16_t* x_f16, const float* x_f32, int t, int H, float* xf) {
+    for (int h = 0; h < H; h++)
+        xf[h] = x_f16 ? oracle_f16_to_f32(x_f16[(size_t)t * H + h]) : x_f32[(size_t)t * H + h];
+}
+
+static int switch_mlp_rows(const oracle_layer* L, const uint16_t* x_f16, const float* x_f32, const int32_t* idx,
+                           int T, int K, float* y, int nthreads) {
     const int H = L->hidden, I = L->inter;
     if (T < 0 || K <= 0 || H % ORACLE_GROUP || I % ORACLE_GROUP || (L->bits != 3 && L->bits != 4)) return -1;
     int nt = nthreads < 1 ? 1 : (nthreads > K ? K : nthreads);
@@ -193,7 +193,7 @@ int oracle_switch_mlp(const oracle_layer* L, const uint16_t* x_f16, const int32_
     }
     int err = 0;
     for (int t = 0; t < T && !err; t++) {
-        for (int h = 0; h < H; h++) xf[h] = oracle_f16_to_f32(x_f16[(size_t)t * H + h]);
+        token_row(x_f16, x_f32, t, H, xf);
         fan_task tasks[64];
         pthread_t th[64];
         if (nt > 64) nt = 64;
@@ -211,6 +211,24 @@ int oracle_switch_mlp(const oracle_layer* L, const uint16_t* x_f16, const int32_
     free(xf);
     free(scr);
     return err ? -1 : 0;
+}
+
+/*
+ * switch_mlp contract (kandiga/engine.py:670-739): y[t, k, :] = expert idx[t, k] applied to x[t].
+ * x is fp16 [T, H] (converted to fp32 as kandiga_cpu_expert.m:670-674), y is fp32 [T, K, H]
+ * (the value bakan_cpu_expert_mlp returns before its fp16 rounding).
+ * nthreads <= 1 runs single-threaded; otherwise each token fans its K experts over
+ * min(K, nthreads) threads and joins before the next token, as the reference does.
+ */
+int oracle_switch_mlp(const oracle_layer* L, const uint16_t* x_f16, const int32_t* idx, int T, int K, float* y,
+                      int nthreads) {
+    return x_f16 ? switch_mlp_rows(L, x_f16, NULL, idx, T, K, y, nthreads) : -1;
+}
+
+/* The same with fp32 activations [T, H] taken as they are (bakan_cpu_expert_mlp). */
+int oracle_switch_mlp_f32(const oracle_layer* L, const float* x_f32, const int32_t* idx, int T, int K, float* y,
+                          int nthreads) {
+    return x_f32 ? switch_mlp_rows(L, NULL, x_f32, idx, T, K, y, nthreads) : -1;
 }
 
 /* fp32 -> fp16 rounding of a buffer (kandiga_cpu_expert.m:681-685). */

@@ -168,7 +168,8 @@ def combine(y: np.ndarray, w: np.ndarray) -> np.ndarray:
 
 
 def silu64(g):
-    return g / (1.0 + np.exp(-g))
+    with np.errstate(over="ignore"):   # exp(-g) = inf for very negative g gives silu = -0, as it should
+        return g / (1.0 + np.exp(-g))
 
 
 def shared_expert_f64(layer: dict, x: np.ndarray) -> np.ndarray:
@@ -206,7 +207,7 @@ def dequantize_dense(words, scales, biases, bits: int, in_dim: int, scale_dtype:
 
 def moe_out_dense(expert_arrays, x: np.ndarray, idx: np.ndarray, w: np.ndarray, bits: int, hidden: int,
                   inter: int, scale_dtype: str = "f16", act: str = "silu", dtype=np.float64,
-                  threads: int = 8) -> np.ndarray:
+                  threads: int = 8, exact_x: bool = False) -> np.ndarray:
     """Routed combine ``out[t] = sum_k w[t,k] * expert_{idx[t,k]}(x[t])`` for every token of a
     full-size batch, through dense matrix products one expert at a time: all the rows routed
     to an expert go through its dequantized gate/up/down matrices together.
@@ -214,13 +215,14 @@ def moe_out_dense(expert_arrays, x: np.ndarray, idx: np.ndarray, w: np.ndarray, 
     ``expert_arrays(e)`` returns expert e's nine arrays (``gate_w``, ``gate_s``, ...,
     ``down_b``, without the expert dimension).  Experts are spread over ``threads`` workers,
     each with a single-threaded BLAS.  float64 by default; float32 keeps the relative error
-    near 1e-6, three orders below the layer tolerance, at half the time."""
+    near 1e-6, three orders below the layer tolerance, at half the time.  ``x`` is rounded to
+    fp16 unless ``exact_x`` (bf16 / fp32 activations, taken as given)."""
     from concurrent.futures import ThreadPoolExecutor
     from threadpoolctl import threadpool_limits
 
     idx = np.asarray(idx)
     T, K = idx.shape
-    xs = np.asarray(x, dtype=np.float16).astype(dtype)
+    xs = np.asarray(x, dtype=dtype if exact_x else np.float16).astype(dtype)
     wts = np.asarray(w, dtype=np.float64)
     experts = np.unique(idx)
 
@@ -233,7 +235,7 @@ def moe_out_dense(expert_arrays, x: np.ndarray, idx: np.ndarray, w: np.ndarray, 
         xr = xs[tok]
         gv, uv = xr @ g.T, xr @ u.T
         if act == "silu":
-            av = gv / (1 + np.exp(-gv)) * uv
+            av = silu64(gv) * uv
         else:
             av = 0.5 * gv * (1 + np.tanh(0.7978845608 * (gv + 0.044715 * gv ** 3))) * uv
         return tok, (av @ d.T).astype(np.float64) * wts[tok, kk][:, None]
@@ -253,12 +255,13 @@ def expert_weights_f64(layer: dict, e: int, bits: int, hidden: int, inter: int, 
 
 
 def expert_mlp_f64(layer: dict, e: int, x: np.ndarray, bits: int, scale_dtype: str = "f16",
-                   act: str = "silu") -> np.ndarray:
-    """One expert on rows of ``x`` via float64 matrix products of the dequantized weights."""
+                   act: str = "silu", exact_x: bool = False) -> np.ndarray:
+    """One expert on rows of ``x`` via float64 matrix products of the dequantized weights (``x``
+    rounded to fp16, or with ``exact_x`` taken as given)."""
     H = layer["gate_s"].shape[-1] * GROUP
     I = layer["down_s"].shape[-1] * GROUP
     g_w, u_w, d_w = expert_weights_f64(layer, e, bits, H, I, scale_dtype)
-    xs = np.atleast_2d(np.asarray(x, dtype=np.float16).astype(np.float64))
+    xs = np.atleast_2d(np.asarray(x, dtype=np.float64 if exact_x else np.float16).astype(np.float64))
     g = xs @ g_w.T
     u = xs @ u_w.T
     if act == "silu":
@@ -299,6 +302,9 @@ def lib():
         L.oracle_switch_mlp.argtypes = [ctypes.POINTER(_Layer), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
         L.oracle_switch_mlp.restype = ctypes.c_int
+        L.oracle_switch_mlp_f32.argtypes = [ctypes.POINTER(_Layer), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+        L.oracle_switch_mlp_f32.restype = ctypes.c_int
         L.oracle_round_f16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
         L.oracle_f32_to_f16.argtypes = [ctypes.c_float]
         L.oracle_f32_to_f16.restype = ctypes.c_uint16
@@ -318,11 +324,18 @@ def _proj(layer, name):
 
 
 def switch_mlp(layer: dict, x: np.ndarray, idx: np.ndarray, bits: int, scale_dtype: str = "f16",
-               act: str = "silu", nthreads: int = 1) -> np.ndarray:
-    """``y[t, k] = expert idx[t, k] (x[t])`` in fp32 via the C restatement -> ``[T, K, H]``."""
+               act: str = "silu", nthreads: int = 1, exact_x: bool = False) -> np.ndarray:
+    """``y[t, k] = expert idx[t, k] (x[t])`` in fp32 via the C restatement -> ``[T, K, H]``.
+
+    ``x`` is rounded to fp16 (``bakan_cpu_expert_mlp_f16``), or with ``exact_x`` taken as fp32
+    values as they are (``bakan_cpu_expert_mlp``; bf16 activations are widened to fp32 exactly
+    and passed this way, as ``bakan_cpu_expert_mlp_bf16`` does)."""
     H = layer["gate_s"].shape[-1] * GROUP
     I = layer["down_s"].shape[-1] * GROUP
-    x16 = np.ascontiguousarray(np.asarray(x, dtype=np.float16)).view(np.uint16)
+    if exact_x:
+        xa = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    else:
+        xa = np.ascontiguousarray(np.asarray(x, dtype=np.float16)).view(np.uint16)
     idx = np.ascontiguousarray(idx, dtype=np.int32)
     T, K = idx.shape
     if idx.size and (idx.min() < 0 or idx.max() >= layer["gate_w"].shape[0]):
@@ -330,8 +343,8 @@ def switch_mlp(layer: dict, x: np.ndarray, idx: np.ndarray, bits: int, scale_dty
     y = np.empty((T, K, H), dtype=np.float32)
     desc = _Layer(H, I, bits, 1 if scale_dtype == "bf16" else 0, 0 if act == "silu" else 1,
                   _proj(layer, "gate"), _proj(layer, "up"), _proj(layer, "down"))
-    rc = lib().oracle_switch_mlp(ctypes.byref(desc), x16.ctypes.data, idx.ctypes.data, T, K, y.ctypes.data,
-                                 int(nthreads))
+    fn = lib().oracle_switch_mlp_f32 if exact_x else lib().oracle_switch_mlp
+    rc = fn(ctypes.byref(desc), xa.ctypes.data, idx.ctypes.data, T, K, y.ctypes.data, int(nthreads))
     if rc != 0:
         raise RuntimeError("oracle_switch_mlp failed")
     return y

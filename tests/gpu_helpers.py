@@ -81,11 +81,12 @@ def host_layer(layer) -> dict:
     return out
 
 
-def dense_reference(layer_h: dict, shape, x, idx, w, scale_dtype="f16", dtype=np.float64):
+def dense_reference(layer_h: dict, shape, x, idx, w, scale_dtype="f16", dtype=np.float64, exact_x=False):
     """Oracle output of every row of a full-size batch: routed combine through dense per-expert
     products (oracle.moe_out_dense) plus the shared expert when the layer has one."""
     out = O.moe_out_dense(lambda e: {k: v[e] for k, v in layer_h.items() if not k.startswith("shared_")},
-                          x, idx, w, shape.bits, shape.hidden, shape.intermediate, scale_dtype, dtype=dtype)
+                          x, idx, w, shape.bits, shape.hidden, shape.intermediate, scale_dtype, dtype=dtype,
+                          exact_x=exact_x)
     if "shared_gate" in layer_h:
         out = out + O.shared_expert_f64(layer_h, x)
     return out

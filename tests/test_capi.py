@@ -128,6 +128,26 @@ def test_calls_validate_before_launch():
     L.kmoe_layer_destroy(h)
 
 
+def test_activation_dtypes_validate_before_launch():
+    """kmoe_forward_x / kmoe_expert_mlp_x: unknown dtypes are refused, and a layer with the dense
+    fp16 shared expert refuses bf16/fp32 activations, all before anything is launched."""
+    L = _capi.lib()
+    null = None
+    rc, h = _create(_desc())
+    assert L.kmoe_forward_x(h, 256, 3, 256, 1, 256, 0, null, null, 256, 1 << 30, null) == _capi.ERR_INVALID_ARG
+    assert L.kmoe_forward_x(h, 256, -1, 256, 1, 256, 0, null, null, 256, 1 << 30, null) == _capi.ERR_INVALID_ARG
+    assert L.kmoe_expert_mlp_x(h, 256, 5, 256, 1, 256, 256, 1 << 30, null) == _capi.ERR_INVALID_ARG
+    assert L.kmoe_forward_x(h, 256, _capi.X_BF16, 256, 0, 256, 0, null, null, 256, 1 << 30, null) == 0
+    assert L.kmoe_forward_x(h, 258, _capi.X_F32, 256, 1, 256, 0, null, null, 256, 1 << 30, null) == _capi.ERR_ALIGNMENT
+    L.kmoe_layer_destroy(h)
+    fake = 1 << 20
+    rc, hs = _create(_desc(shared_gate=fake, shared_up=fake, shared_down=fake, shared_intermediate=1024))
+    assert rc == 0
+    assert L.kmoe_forward_x(hs, 256, _capi.X_BF16, 256, 1, 256, 0, null, null, 256, 1 << 30, null) == \
+        _capi.ERR_UNSUPPORTED
+    L.kmoe_layer_destroy(hs)
+
+
 def test_prefill_copy_size_and_validation():
     L = _capi.lib()
     n = ctypes.c_size_t()

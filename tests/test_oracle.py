@@ -416,3 +416,38 @@ def test_moe_block_composition_closed_form():
     assert np.abs(sh16 - sh).max() > 0                       # the shared output is rounded
     assert np.abs(r["out"] - (want - res)).max() > 1.0       # the residual is in
     assert np.abs(0.5 * sh16).max() > 1e-2                   # the gated shared term matters
+
+
+# ---- fp32 / bf16 activations (bakan_cpu_expert_mlp, bakan_cpu_expert_mlp_bf16) --------------
+def test_switch_mlp_fp32_path_equals_fp16_path_on_fp16_values():
+    """The fp32-activation entry widens nothing: on fp16-representable x it runs the same fp32
+    arithmetic as the fp16 entry, bit for bit."""
+    shape = synth.LayerShape(128, 64, 6, 3, 3)
+    layer = synth.make_layer(shape, 71)
+    x, logits = synth.make_inputs(shape, 4, 72)
+    idx, _ = O.route(logits, 3)
+    a = O.switch_mlp(layer, x, idx, 3)
+    b = O.switch_mlp(layer, x.astype(np.float32), idx, 3, exact_x=True)
+    assert np.array_equal(a, b)
+
+
+def test_switch_mlp_fp32_activations_against_f64():
+    """General fp32 x (not fp16-representable, several magnitudes) against float64 products of
+    the dequantized matrices on the same fp32 values; and the batched dense oracle agrees."""
+    shape = synth.LayerShape(128, 64, 6, 3, 4)
+    layer = synth.make_layer(shape, 73)
+    rng = np.random.default_rng(74)
+    x = (rng.standard_normal((3, 128)) * np.array([[1.0], [300.0], [1e-3]])).astype(np.float32)
+    assert not np.array_equal(x, x.astype(np.float16).astype(np.float32))
+    _, logits = synth.make_inputs(shape, 3, 75)
+    idx, w = O.route(logits, 3)
+    y = O.switch_mlp(layer, x, idx, 4, exact_x=True)
+    for t in range(3):
+        for k in range(3):
+            ref = O.expert_mlp_f64(layer, idx[t, k], x[t], 4, exact_x=True)[0]
+            np.testing.assert_allclose(y[t, k], ref, rtol=2e-5, atol=2e-5 * np.abs(ref).max())
+    dense = O.moe_out_dense(lambda e: {k: v[e] for k, v in layer.items()}, x, idx, w, 4, 128, 64, exact_x=True)
+    np.testing.assert_allclose(O.combine(y, w), dense, rtol=2e-5, atol=2e-5 * np.abs(dense).max())
+    # rounding x to fp16 instead moves the result past the bar above: the check can tell them apart
+    y16 = O.switch_mlp(layer, x, idx, 4)
+    assert np.abs(y16 - y).max() > 2e-5 * np.abs(y).max()
