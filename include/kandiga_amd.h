@@ -235,7 +235,7 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
  * kandiga/tq3/convert_experts.py:140-200: per expert the gate [I][H], up [I][H] and down [H][I]
  * matrices in turn, expert_bytes apart): y[t][k] = down(silu(gate x_t) * (up x_t)) of expert
  * idx[t][k], fp16.  Experts outside [0, num_experts) give zero rows.  The workspace holds the
- * gate/up outputs (kmoe_tq3_workspace_size).
+ * SwiGLU outputs (kmoe_tq3_workspace_size).
  */
 int kmoe_tq3_gemv(const void* blocks, int32_t rows, int32_t cols, const void* x, int32_t x_f32, int32_t tokens,
                   float* out, void* stream);

@@ -542,15 +542,16 @@ int kmoe_tq3_gemv(const void* blocks, int32_t rows, int32_t cols, const void* x,
     return fail(KMOE_ERR_INVALID_ARG, "rows/tokens must be >= 0 and cols a multiple of 32 up to 4096");
   if (rows == 0 || tokens == 0) return ok();
   if (!blocks || !x || !out) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
-  if (!aligned(blocks, 4) || !aligned(x, 4) || !aligned(out, 4)) return fail(KMOE_ERR_ALIGNMENT, "pointers must be 4-byte aligned");
-  Tq3Params p{static_cast<const uint8_t*>(blocks), 0, 0, 0, rows, nullptr, 1, x, 1, tokens, rows, cols, out, nullptr};
-  hipError_t e = launch_tq3_gemv(p, x_f32 ? 1 : 0, static_cast<hipStream_t>(stream));
+  if (!aligned(blocks, 4) || !aligned(x, 16) || !aligned(out, 4))
+    return fail(KMOE_ERR_ALIGNMENT, "blocks and out must be 4-byte aligned, x 16-byte aligned");
+  Tq3Params p{static_cast<const uint8_t*>(blocks), 0, 0, nullptr, 1, x, 1, tokens, rows, cols, out, nullptr};
+  hipError_t e = launch_tq3_gemv(p, x_f32 != 0, false, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? ok() : hip_fail(e, "tq3 gemv launch");
 }
 
 int kmoe_tq3_workspace_size(int32_t tokens, int32_t top_k, int32_t intermediate, size_t* bytes) {
   if (!bytes || tokens < 0 || top_k < 1 || intermediate <= 0) return fail(KMOE_ERR_INVALID_ARG, "bad sizes");
-  *bytes = up256((size_t)tokens * top_k * 2 * intermediate * sizeof(float));
+  *bytes = up256((size_t)tokens * top_k * intermediate * sizeof(float));
   return ok();
 }
 
@@ -564,24 +565,22 @@ int kmoe_tq3_expert_mlp(const void* experts, int64_t expert_bytes, int32_t num_e
   if (expert_bytes < 3 * mat) return fail(KMOE_ERR_INVALID_ARG, "expert_bytes below the three TQ3 matrices");
   if (tokens == 0) return ok();
   if (!experts || !x || !idx || !y || !workspace) return fail(KMOE_ERR_INVALID_ARG, "null pointer");
-  if (!aligned(experts, 4) || expert_bytes % 4 || !aligned(x, 4) || !aligned(y, 4) || !aligned(idx, 4) ||
-      !aligned(workspace, 4))
-    return fail(KMOE_ERR_ALIGNMENT, "pointers and expert_bytes must be 4-byte aligned");
+  if (!aligned(experts, 4) || expert_bytes % 4 || !aligned(x, 16) || !aligned(y, 4) || !aligned(idx, 4) ||
+      !aligned(workspace, 16))
+    return fail(KMOE_ERR_ALIGNMENT, "experts/expert_bytes/y/idx 4-byte aligned, x and workspace 16-byte aligned");
   size_t need = 0;
   kmoe_tq3_workspace_size(tokens, top_k, intermediate, &need);
   if (workspace_bytes < need) return fail(KMOE_ERR_WORKSPACE, "workspace has %zu bytes, needs %zu", workspace_bytes, need);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  float* gu = static_cast<float*>(workspace);
-  const uint8_t* w = static_cast<const uint8_t*>(experts);
   const int V = tokens * top_k;
-  // gate rows then up rows of every (token, k), gate/up pairs [V][2I] fp32
-  Tq3Params a{w, expert_bytes, 0, mat, intermediate, idx, num_experts, x, top_k, V, 2 * intermediate, hidden, gu,
-              nullptr};
-  hipError_t e = launch_tq3_gemv(a, 0, s);
-  // down projection of silu(g)*u, fp16 y [V][H]
-  Tq3Params d{w, expert_bytes, 2 * mat, 2 * mat, hidden, idx, num_experts, gu, 1, V, hidden, intermediate, nullptr,
+  float* act = static_cast<float*>(workspace);
+  const uint8_t* w = static_cast<const uint8_t*>(experts);
+  // gate/up pairs with the SwiGLU output act [V][I] fp32, then down to fp16 y [V][H]
+  Tq3Params a{w, expert_bytes, mat, idx, num_experts, x, top_k, V, intermediate, hidden, act, nullptr};
+  hipError_t e = launch_tq3_gemv(a, false, true, s);
+  Tq3Params d{w + 2 * mat, expert_bytes, 0, idx, num_experts, act, 1, V, hidden, intermediate, nullptr,
               static_cast<uint16_t*>(y)};
-  if (e == hipSuccess) e = launch_tq3_gemv(d, 2, s);
+  if (e == hipSuccess) e = launch_tq3_gemv(d, true, false, s);
   return e == hipSuccess ? ok() : hip_fail(e, "tq3 expert mlp launch");
 }
 

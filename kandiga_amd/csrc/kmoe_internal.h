@@ -179,14 +179,13 @@ hipError_t launch_qlinear(const QProj& a, int ra, const QProj& b, int rb, int bi
 hipError_t launch_blend_prep(const uint16_t* shared16, const float* gate, const uint16_t* residual, int T, int H,
                              float* extra, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t s);
-// TQ3 GEMV (tq3.hip): out[v][r] = row r of the TQ3 matrix of expert vexp[v] applied to input vector v
-// (input row v / in_div); rows < rsplit read the matrix at moff0 inside the expert body, the others
-// the one at moff1.  mode 0: fp16 inputs [*][C]; 1: fp32 inputs; 2: silu(g)*u of fp32 rows [g | u]
-// of 2C.  Experts outside [0, E) give zeros.  C a multiple of 32 up to 4096.
+// TQ3 GEMV (tq3.hip): out[v][r] = row r of the TQ3 matrix of expert vexp[v] (at w + e * wstride;
+// null vexp: expert 0) dotted with input row v / in_div (fp16, or fp32 when in32; rotated by the
+// kernel); pair: r indexes gate/up row pairs (up matrix at + up_off) and out = silu(gate) * up.
+// fp32 or fp16 out; experts outside [0, E) give zeros.  C a multiple of 32 up to 4096.
 struct Tq3Params {
   const uint8_t* w;
-  int64_t wstride, moff0, moff1;
-  int rsplit;
+  int64_t wstride, up_off;
   const int32_t* vexp;
   int E;
   const void* in;
@@ -194,7 +193,7 @@ struct Tq3Params {
   float* out32;
   uint16_t* out16;
 };
-hipError_t launch_tq3_gemv(const Tq3Params& p, int mode, hipStream_t s);
+hipError_t launch_tq3_gemv(const Tq3Params& p, bool in32, bool pair, hipStream_t s);
 // Writes the prefill copy of c's experts into `pack` (laid out by pack_layout).
 hipError_t launch_prefill_pack(const LayerConfig& c, uint8_t* pack, hipStream_t s);
 hipError_t launch_dequantize(const LayerConfig& c, int proj, int expert, int row0, int nrows, uint8_t* codes,

@@ -100,7 +100,10 @@ static void abi_checks() {
         KMOE_ERR_INVALID_ARG);
   CHECK(kmoe_prefill_pack_size(&d, &np) == KMOE_OK && np > 0);
   CHECK(kmoe_tq3_gemv(fake, 64, 48, fake, 0, 1, (float*)fake, nullptr) == KMOE_ERR_INVALID_ARG);
+  CHECK(kmoe_tq3_gemv(fake, 64, 64, (char*)fake + 4, 0, 1, (float*)fake, nullptr) == KMOE_ERR_ALIGNMENT);
   CHECK(kmoe_tq3_workspace_size(1, 0, 512, &np) == KMOE_ERR_INVALID_ARG);
+  CHECK(kmoe_tq3_expert_mlp(fake, 3 * 2048 * 512 / 32 * 20, 4, 2048, 512, fake, (const int32_t*)fake, 2, 8, fake, fake,
+                            1024, nullptr) == KMOE_ERR_WORKSPACE);
   CHECK(kmoe_tq3_expert_mlp(fake, 100, 4, 2048, 512, fake, (const int32_t*)fake, 1, 8, fake, fake, 1 << 20, nullptr) ==
         KMOE_ERR_INVALID_ARG);
   CHECK(kmoe_profile_begin(0) == KMOE_ERR_INVALID_ARG);
