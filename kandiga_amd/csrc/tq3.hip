@@ -20,7 +20,6 @@
 namespace kmoe {
 
 constexpr int TQ3_BLOCK = 32, TQ3_BYTES = 20;
-constexpr int TQ3_UR = 4;  // rows of a wave whose weight loads are in flight together
 
 __constant__ float c_tq3_cent[8] = {-1.996684f, -1.291398f, -0.740341f, -0.247508f,
                                     0.230106f,  0.725222f,  1.277503f,  1.988943f};
@@ -181,10 +180,10 @@ struct Tq3Gemv {
 // out[v][r] for rows r of one workgroup: row r of expert vexp[v]'s matrix dotted with input row
 // v / in_div, rotated into LDS by the workgroup (experts outside [0, E) give zeros).  PAIR: output
 // r is silu(gate row r . x) * (up row r . x), the two dots in the same lanes.  Wave w takes row
-// groups r0 + RPI*(w + 4j) (RPI = 64 / LPR rows at a time), UR groups per pass: every weight load
-// of the pass is issued before the input's rotation, so the rotation runs while they are in
-// flight.
-template <int CPL, bool IN32, bool PAIR>
+// groups r0 + RPI*(w + 4j) (RPI = 64 / LPR rows at a time), UR groups per pass whose weight
+// loads are in flight together: every weight load of the pass is issued before the input's
+// rotation, so the rotation runs while they are in flight.
+template <int CPL, bool IN32, bool PAIR, int UR>
 __global__ __launch_bounds__(256) void tq3_gemv_kernel(const Tq3Gemv P) {
   extern __shared__ float lds[];  // [C] rotated input, [C/16] half sums
   __shared__ float s_cent[8];
@@ -206,10 +205,10 @@ __global__ __launch_bounds__(256) void tq3_gemv_kernel(const Tq3Gemv P) {
   const int r0 = blockIdx.x * P.rows_per_wg;
   const int ir = v / P.in_div;
   bool first = true;
-  for (int base = wave * rpi; base < P.rows_per_wg; base += 4 * rpi * TQ3_UR) {
-    Tq3W<CPL> W[TQ3_UR][ND];
+  for (int base = wave * rpi; base < P.rows_per_wg; base += 4 * rpi * UR) {
+    Tq3W<CPL> W[UR][ND];
 #pragma unroll
-    for (int u = 0; u < TQ3_UR; ++u) {
+    for (int u = 0; u < UR; ++u) {
       const int rr = base + 4 * rpi * u + rl, row = r0 + rr;
       const bool on = valid && rr < P.rows_per_wg && row < P.R;
 #pragma unroll
@@ -225,7 +224,7 @@ __global__ __launch_bounds__(256) void tq3_gemv_kernel(const Tq3Gemv P) {
     Tq3X<CPL> X;
     load_lane_x<CPL>(s_xr, s_hs, cl, lpr, nb, X);
 #pragma unroll
-    for (int u = 0; u < TQ3_UR; ++u) {
+    for (int u = 0; u < UR; ++u) {
       const int rr = base + 4 * rpi * u + rl, row = r0 + rr;
       float tot = group_sum_last(lane_dot<CPL>(W[u][0], X, s_cent), lpr);
       if constexpr (PAIR) tot = silu_f32(tot) * group_sum_last(lane_dot<CPL>(W[u][1], X, s_cent), lpr);
@@ -252,15 +251,24 @@ hipError_t launch_tq3_gemv(const Tq3Params& a, bool in32, bool pair, hipStream_t
   if (a.C % TQ3_BLOCK || a.C > 4096) return hipErrorInvalidValue;
   Tq3Gemv P{a.w, a.wstride, a.up_off, a.vexp, a.E, a.in, a.in_div, a.V, a.R, a.C, 0, a.out32, a.out16};
   const int nb = a.C / TQ3_BLOCK;
-  // one pass of the four waves per workgroup, passes added while the grid keeps >= 512 workgroups
-  const int step = 4 * (64 / tq3_lpr(nb)) * TQ3_UR;
-  int passes = 1;
-  while (passes < 8 && (long long)a.V * ((a.R + step * passes * 2 - 1) / (step * passes * 2)) >= 512) passes *= 2;
-  P.rows_per_wg = step * passes;
+  // One pass of the four waves per workgroup, UR row groups each.  A grid that would stay under
+  // 512 workgroups with four groups per wave takes two (twice the workgroups: one token's gate/up
+  // 10.6 -> 8.8 us); a grid that stays at 1024 workgroups or more takes two or more passes.
+  const int rpi = 64 / tq3_lpr(nb);
+  auto wgs = [&](int rows) { return (long long)a.V * ((a.R + rows - 1) / rows); };
+  const bool ur2 = wgs(16 * rpi) < 512;
+  const int step = 4 * rpi * (ur2 ? 2 : 4);
+  P.rows_per_wg = step;
+  while (!ur2 && P.rows_per_wg < 8 * step && wgs(2 * P.rows_per_wg) >= 1024) P.rows_per_wg *= 2;
   const dim3 grid((a.R + P.rows_per_wg - 1) / P.rows_per_wg, a.V);
   const uint32_t lds = (uint32_t)(a.C + a.C / 16) * sizeof(float);
-#define KMOE_TQ(CPLV, IN32V, PAIRV) \
-  KMOE_LAUNCH("tq3_gemv_kernel", (tq3_gemv_kernel<CPLV, IN32V, PAIRV>), grid, dim3(256), lds, s, P)
+#define KMOE_TQ(CPLV, IN32V, PAIRV)                                                                        \
+  do {                                                                                                    \
+    if (ur2)                                                                                              \
+      KMOE_LAUNCH("tq3_gemv_kernel", (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 2>), grid, dim3(256), lds, s, P); \
+    else                                                                                                  \
+      KMOE_LAUNCH("tq3_gemv_kernel", (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 4>), grid, dim3(256), lds, s, P); \
+  } while (0)
   if (nb > 64) {
     if (pair) KMOE_TQ(2, false, true);
     else if (in32) KMOE_TQ(2, true, false);
