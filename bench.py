@@ -78,6 +78,8 @@ def parse():
                    help="skip the 4096-token prefill of the hidden-4096 / 512-expert layer")
     p.add_argument("--no-stack60", dest="stack60", action="store_false",
                    help="skip the 60-layer hidden-4096 / 512-expert / top-10 decode stack (~169 GB resident)")
+    p.add_argument("--no-tq3", dest="tq3", action="store_false",
+                   help="skip the TQ3 codebook expert MLP at 1 and 4 tokens")
     p.add_argument("--no-4bit", dest="four_bit", action="store_false",
                    help="skip the 4-bit decode layer (GPU and CPU)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -352,6 +354,14 @@ def main():
         del ex1
         torch.cuda.empty_cache()
 
+    # TQ3 codebook experts of the same shape (hidden 2048, 256 experts, intermediate 512, top-8):
+    # the switch_mlp contract through kmoe_tq3_expert_mlp, graph-replayed over 3 layers with
+    # enough token inputs that one pass touches over 1 GiB of distinct expert bytes
+    if args.tq3 and args.decode:
+        experts.clear()
+        torch.cuda.empty_cache()
+        results.update(tq3_cases(torch, dev, shape, args.steps, profile_kernels, log))
+
     head = results.get("decode_T1_K8_graph") or next(iter(results.values()), None)
     if head is None:
         print(json.dumps({"metric": METRIC, "detail": prefill}), flush=True)
@@ -401,6 +411,82 @@ def main():
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def tq3_cases(torch, dev, shape, steps, profile_kernels, log) -> dict:
+    """The TQ3 expert MLP (switch_mlp contract, fp16 x, top-8) at 1 and 4 tokens on three seeded
+    layers of 256 TQ3 experts (hidden 2048, intermediate 512; random indices, fp16 block scales
+    in [0, 0.02)), captured as one graph over enough inputs per layer that a replay touches
+    >= 1 GiB of distinct expert bytes.  GB/s counts the distinct experts' bytes per call plus x
+    and y; per-kernel figures come from HIP events around each launch in an eager pass."""
+    from kandiga_amd import tq3
+
+    H, I, E, K = shape.hidden, shape.intermediate, shape.num_experts, 8
+    eb = tq3.expert_bytes(H, I)
+    g = torch.Generator(device=dev)
+    g.manual_seed(8100)
+    layers = []
+    for _ in range(3):
+        body = torch.randint(0, 256, (E, eb), dtype=torch.uint8, device=dev, generator=g)
+        blk = body.view(E, -1, 20)
+        for j in range(0, E, 32):  # the four fp16 block scales, in chunks to bound the temporary
+            sc = (torch.rand((min(32, E - j), blk.shape[1], 4), device=dev, generator=g) * 0.02).half()
+            blk[j:j + 32, :, :8] = sc.view(torch.uint8)
+        layers.append(tq3.TQ3Experts(body, H, I, dev))
+    out = {}
+    for T in (1, 4):
+        for ex in layers:
+            ex.reserve(T, K)
+        seq, seen, uniq = [], [set() for _ in layers], []
+        p = 0
+        while p < 256:
+            for li, ex in enumerate(layers):
+                x = (torch.randn((T, H), device=dev, generator=g) * 0.5).half()
+                idx = torch.rand((T, E), device=dev, generator=g).argsort(dim=1)[:, :K].to(torch.int32).contiguous()
+                ids = torch.unique(idx).tolist()
+                seen[li].update(ids)
+                uniq.append(len(ids))
+                seq.append((ex, x, idx))
+            p += 1
+            if sum(len(q) for q in seen) * eb >= 2 ** 30:
+                break
+        n = len(seq)
+        for ex, x, idx in seq:
+            ex(x, idx)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for ex, x, idx in seq:
+                ex(x, idx)
+        reps = max(5, -(-steps // n))
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * n)
+        U = sum(uniq) / n
+        ba = U * eb + T * H * 2 + T * K * H * 2
+        r = {"T": T, "k": K, "us_per_call": us, "gbs": ba / (us * 1e-6) / 1e9, "bytes_alg": ba,
+             "unique_experts": U, "calls": reps * n, "inputs_per_layer": p,
+             "distinct_expert_bytes_per_replay": sum(len(q) for q in seen) * eb}
+        with profile_kernels(4 * n + 16) as prof:
+            for ex, x, idx in seq:
+                ex(x, idx)
+        kern = {}
+        for name, v in prof.result.items():
+            kern[name] = {"mean_us": v["mean_ms"] * 1e3, "launches": v["launches"]}
+        launches = sorted(kern.items(), key=lambda kv: -kv[1]["mean_us"])
+        r["kernels"] = kern
+        out[f"tq3_T{T}_K{K}_graph"] = r
+        log(f"TQ3 expert MLP T={T} K={K}: {us:.2f} us/call  {r['gbs']:.0f} GB/s  U={U:.1f} P={p}  "
+            + "  ".join(f"{nm} {v['mean_us']:.2f} us x{v['launches']}" for nm, v in launches))
+    del layers
+    torch.cuda.empty_cache()
+    return out
 
 
 def measured_copy_gbs(torch, dev) -> float:

@@ -262,12 +262,14 @@ hipError_t launch_tq3_gemv(const Tq3Params& a, bool in32, bool pair, hipStream_t
   while (!ur2 && P.rows_per_wg < 8 * step && wgs(2 * P.rows_per_wg) >= 1024) P.rows_per_wg *= 2;
   const dim3 grid((a.R + P.rows_per_wg - 1) / P.rows_per_wg, a.V);
   const uint32_t lds = (uint32_t)(a.C + a.C / 16) * sizeof(float);
-#define KMOE_TQ(CPLV, IN32V, PAIRV)                                                                        \
-  do {                                                                                                    \
-    if (ur2)                                                                                              \
-      KMOE_LAUNCH("tq3_gemv_kernel", (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 2>), grid, dim3(256), lds, s, P); \
-    else                                                                                                  \
-      KMOE_LAUNCH("tq3_gemv_kernel", (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 4>), grid, dim3(256), lds, s, P); \
+  // profiler names: the expert MLP's two launches apart
+  const char* name = pair ? "tq3_gemv_kernel:gate_up" : in32 ? "tq3_gemv_kernel:down" : "tq3_gemv_kernel";
+#define KMOE_TQ(CPLV, IN32V, PAIRV)                                                                 \
+  do {                                                                                             \
+    if (ur2)                                                                                       \
+      KMOE_LAUNCH(name, (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 2>), grid, dim3(256), lds, s, P);     \
+    else                                                                                           \
+      KMOE_LAUNCH(name, (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 4>), grid, dim3(256), lds, s, P);     \
   } while (0)
   if (nb > 64) {
     if (pair) KMOE_TQ(2, false, true);

@@ -194,6 +194,25 @@ class TQ3Experts:
         if self.body.shape[1] != expert_bytes(hidden, inter):
             raise ValueError("expert body size does not match hidden/intermediate")
         self._ws = None
+        self._ws_retired = []  # earlier workspaces, kept alive for graphs captured with them
+
+    def reserve(self, tokens: int, top_k: int) -> None:
+        """Allocate the workspace for calls of up to ``tokens`` x ``top_k`` assignments (do this
+        before capturing calls into a graph; growing under a capture is refused)."""
+        import torch
+
+        from . import _capi
+
+        n = ctypes.c_size_t()
+        _capi.check(_capi.lib().kmoe_tq3_workspace_size(int(tokens), int(top_k), self.intermediate, ctypes.byref(n)),
+                    "kmoe_tq3_workspace_size")
+        if self._ws is None or self._ws.numel() < n.value:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"TQ3 workspace for {tokens}x{top_k} assignments was not reserved before graph "
+                                   "capture; call reserve() first")
+            if self._ws is not None:
+                self._ws_retired.append(self._ws)
+            self._ws = torch.empty(max(n.value, 256), dtype=torch.uint8, device=self.device)
 
     @classmethod
     def from_file(cls, path: str, device="cuda") -> "TQ3Experts":
@@ -215,14 +234,12 @@ class TQ3Experts:
         if idx.shape[0] != T:
             raise ValueError("x and indices disagree on the number of tokens")
         L = _capi.lib()
-        n = ctypes.c_size_t()
-        _capi.check(L.kmoe_tq3_workspace_size(T, K, self.intermediate, ctypes.byref(n)), "kmoe_tq3_workspace_size")
-        if self._ws is None or self._ws.numel() < n.value:
-            self._ws = torch.empty(max(n.value, 256), dtype=torch.uint8, device=self.device)
+        self.reserve(T, K)
         y = torch.empty((T, K, self.hidden), dtype=torch.float16, device=self.device)
         _capi.check(L.kmoe_tq3_expert_mlp(self.body.data_ptr(), self.body.shape[1], self.num_experts, self.hidden,
                                           self.intermediate, xf.data_ptr(), idx.data_ptr(), T, K, y.data_ptr(),
-                                          self._ws.data_ptr(), self._ws.numel(), _stream()), "kmoe_tq3_expert_mlp")
+                                          self._ws.data_ptr(), self._ws.numel(), _stream(self.device)),
+                    "kmoe_tq3_expert_mlp")
         return y.reshape(*indices.shape, self.hidden)
 
 
