@@ -136,21 +136,26 @@ struct Stage1Args {
 // activations): the dots run on the scaled hi plane (and, for fp32, the lo plane as a second
 // dot), the gate/up totals are multiplied by 2^-s before the activation, act is stored times
 // 2^2s, and 2^-s goes to xinv[t] for stage 2.
+//
+// The values the first loads need (logits, x, the sizes) come as leading scalar arguments: gfx950
+// preloads those into SGPRs at wave launch (the library is built with kernel-argument preload),
+// so the x and logits loads issue without waiting for the kernel-argument fetch.
 template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE, bool XS>
-__global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
+__global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict__ logits,
+                                                         const void* __restrict__ x, int H, int E, int K, int I,
+                                                         int wgs_per_token, const Stage1Args A) {
   const LayerArgs& L = A.L;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int K = A.K, H = L.H, I = L.I, E = L.E;
   const int nch = H / CHUNK;
-  const int t = blockIdx.x / A.wgs_per_token;
-  const int lb = blockIdx.x - t * A.wgs_per_token;
+  const int t = blockIdx.x / wgs_per_token;
+  const int lb = blockIdx.x - t * wgs_per_token;
   KMOE_MARK(0, 0);
   // the lane's activation chunks as stored: 16 words per chunk (fp16, bf16) or 32 (fp32); XS
   // instantiates the scaled (bf16 / fp32) form, the fp16 form keeps none of its work
   const int xdt = XS ? A.xdt : XDT_F16;
   const bool has_lo = XS && xdt == XDT_F32;
   const int eb = has_lo ? 4 : 2;
-  const char* const xrow = static_cast<const char*>(A.x) + (size_t)t * H * eb;
+  const char* const xrow = static_cast<const char*>(x) + (size_t)t * H * eb;
   uint32_t xw[CPL][32];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
   __shared__ int32_t s_sel[16];
   if (ROUTE && wave == 0) {
     float myw;
-    KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(A.logits + (size_t)t * E, E, K, my, myw)));
+    KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(logits + (size_t)t * E, E, K, my, myw)));
     if (lane < K) {
       s_sel[lane] = my;
       if (lb == 0) {
@@ -382,7 +387,7 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
     KMOE_MARK(0, 4);
   };
   WStage W0, W1;
-  const int step = A.wgs_per_token;
+  const int step = wgs_per_token;
   int item = lb;
   if (item < nitems) load_item(item, W0);
   for (; item < nitems; item += 2 * step) {
@@ -403,13 +408,14 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const Stage1Args A) {
 // unit's loads in flight while the current one is computed); otherwise UF units at a time
 // have all their loads in flight.  Per-assignment row results go to LDS and the combine
 // sums them in k order (moe_block.metal:515-539), so the result does not depend on timing.
+// The routing pointers and the sizes lead the arguments (preloaded into SGPRs, as for stage 1).
 template <int BITS, bool BF16, int S2_ROWS, int RPW, int UF, bool COMBINE>
-__global__ __launch_bounds__(256) void dec_stage2_kernel(const LayerArgs L, int T, int K,
-                                                         const int32_t* __restrict__ idx,
-                                                         const float* __restrict__ wts,
+__global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restrict__ idx,
+                                                         const float* __restrict__ wts, int T, int K, int TG,
+                                                         int lpa_log2, const LayerArgs L,
                                                          const uint16_t* __restrict__ act, size_t act_plane,
                                                          void* __restrict__ out, int out32,
-                                                         const float* __restrict__ shared_out, int lpa_log2, int TG,
+                                                         const float* __restrict__ shared_out,
                                                          const float* __restrict__ xinv) {
   __shared__ float red[DEC_STAGE2_ASSIGN * S2_ROWS];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -703,7 +709,8 @@ static int lpa_log2_for(int I) {
 
 template <typename KERN>
 static hipError_t launch_stage1(KERN k1, int grid, hipStream_t s, const Stage1Args& A) {
-  KMOE_LAUNCH("dec_stage1_kernel", k1, dim3(grid), dim3(256), 0, s, A);
+  KMOE_LAUNCH("dec_stage1_kernel", k1, dim3(grid), dim3(256), 0, s, A.logits, A.x, A.L.H, A.L.E, A.K, A.L.I,
+              A.wgs_per_token, A);
   return hipGetLastError();
 }
 
@@ -758,12 +765,12 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
     constexpr int SR = decltype(srows)::value, RP = decltype(rpw)::value, UF = 2;
     const dim3 grid2(L.H / SR, (T + TG - 1) / TG);
     if (d.combine) {
-      KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, true>), grid2, dim3(256), 0, s, L,
-                  T, K, idx, d.wts, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, l2, TG, A.xinv);
+      KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, true>), grid2, dim3(256), 0, s, idx,
+                  d.wts, T, K, TG, l2, L, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, A.xinv);
     } else {
       KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, false>), grid2, dim3(256), 0, s,
-                  L, T, K, idx, (const float*)nullptr, (const uint16_t*)w.act, A.act_plane, d.out, 0,
-                  (const float*)nullptr, l2, TG, A.xinv);
+                  idx, (const float*)nullptr, T, K, TG, l2, L, (const uint16_t*)w.act, A.act_plane, d.out, 0,
+                  (const float*)nullptr, A.xinv);
     }
   };
   using I4 = std::integral_constant<int, 4>;

@@ -183,41 +183,46 @@ struct Tq3Gemv {
 // groups r0 + RPI*(w + 4j) (RPI = 64 / LPR rows at a time), UR groups per pass whose weight
 // loads are in flight together: every weight load of the pass is issued before the input's
 // rotation, so the rotation runs while they are in flight.
+// The fields the first loads need lead the arguments as scalars, so gfx950 preloads them into
+// SGPRs at wave launch (the library is built with kernel-argument preload).
 template <int CPL, bool IN32, bool PAIR, int UR>
-__global__ __launch_bounds__(256) void tq3_gemv_kernel(const Tq3Gemv P) {
+__global__ __launch_bounds__(256) void tq3_gemv_kernel(const uint8_t* __restrict__ w, const int32_t* __restrict__ vexp,
+                                                       const void* __restrict__ in, int64_t wstride, int64_t up_off,
+                                                       int E, int in_div, int R, int C, int rows_per_wg,
+                                                       const Tq3Gemv P) {
   extern __shared__ float lds[];  // [C] rotated input, [C/16] half sums
   __shared__ float s_cent[8];
   constexpr int ND = PAIR ? 2 : 1;  // row dots per output row
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int v = blockIdx.y;
-  const int nb = P.C / TQ3_BLOCK;
+  const int nb = C / TQ3_BLOCK;
   float* s_xr = lds;
-  float* s_hs = lds + P.C;
+  float* s_hs = lds + C;
   if (tid < 8) s_cent[tid] = c_tq3_cent[tid];
   int lpr = 1;
   while (lpr < nb && lpr < 64) lpr <<= 1;
   const int rpi = 64 / lpr;
   const int cl = lane & (lpr - 1), rl = lane / lpr;
-  const int e = P.vexp ? P.vexp[v] : 0;
-  const bool valid = e >= 0 && e < P.E;
-  const uint8_t* body = P.w + (valid ? (size_t)e * P.wstride : 0);
+  const int e = vexp ? vexp[v] : 0;
+  const bool valid = e >= 0 && e < E;
+  const uint8_t* body = w + (valid ? (size_t)e * wstride : 0);
   const size_t rbytes = (size_t)nb * TQ3_BYTES;
-  const int r0 = blockIdx.x * P.rows_per_wg;
-  const int ir = v / P.in_div;
+  const int r0 = blockIdx.x * rows_per_wg;
+  const int ir = v / in_div;
   bool first = true;
-  for (int base = wave * rpi; base < P.rows_per_wg; base += 4 * rpi * UR) {
+  for (int base = wave * rpi; base < rows_per_wg; base += 4 * rpi * UR) {
     Tq3W<CPL> W[UR][ND];
 #pragma unroll
     for (int u = 0; u < UR; ++u) {
       const int rr = base + 4 * rpi * u + rl, row = r0 + rr;
-      const bool on = valid && rr < P.rows_per_wg && row < P.R;
+      const bool on = valid && rr < rows_per_wg && row < R;
 #pragma unroll
       for (int q = 0; q < ND; ++q)
-        load_lane_w<CPL>(body + (q ? P.up_off : 0) + (size_t)row * rbytes, cl, lpr, nb, on, W[u][q]);
+        load_lane_w<CPL>(body + (q ? up_off : 0) + (size_t)row * rbytes, cl, lpr, nb, on, W[u][q]);
     }
     if (first) {  // uniform: every wave takes at least one pass (rows_per_wg >= 4 * rpi)
       for (int b = tid; b < nb; b += 256)
-        rotate_block_to_lds<IN32>(P.in, (size_t)ir * P.C + (size_t)b * TQ3_BLOCK, s_xr, s_hs, b);
+        rotate_block_to_lds<IN32>(in, (size_t)ir * C + (size_t)b * TQ3_BLOCK, s_xr, s_hs, b);
       __syncthreads();
       first = false;
     }
@@ -228,11 +233,11 @@ __global__ __launch_bounds__(256) void tq3_gemv_kernel(const Tq3Gemv P) {
       const int rr = base + 4 * rpi * u + rl, row = r0 + rr;
       float tot = group_sum_last(lane_dot<CPL>(W[u][0], X, s_cent), lpr);
       if constexpr (PAIR) tot = silu_f32(tot) * group_sum_last(lane_dot<CPL>(W[u][1], X, s_cent), lpr);
-      if (cl == lpr - 1 && rr < P.rows_per_wg && row < P.R) {
+      if (cl == lpr - 1 && rr < rows_per_wg && row < R) {
         if (P.out16)
-          P.out16[(size_t)v * P.R + row] = f32_to_f16_bits(tot);
+          P.out16[(size_t)v * R + row] = f32_to_f16_bits(tot);
         else
-          P.out32[(size_t)v * P.R + row] = tot;
+          P.out32[(size_t)v * R + row] = tot;
       }
     }
   }
@@ -267,9 +272,11 @@ hipError_t launch_tq3_gemv(const Tq3Params& a, bool in32, bool pair, hipStream_t
 #define KMOE_TQ(CPLV, IN32V, PAIRV)                                                                 \
   do {                                                                                             \
     if (ur2)                                                                                       \
-      KMOE_LAUNCH(name, (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 2>), grid, dim3(256), lds, s, P);     \
-    else                                                                                           \
-      KMOE_LAUNCH(name, (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 4>), grid, dim3(256), lds, s, P);     \
+      KMOE_LAUNCH(name, (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 2>), grid, dim3(256), lds, s, P.w, P.vexp, P.in, \
+                  P.wstride, P.up_off, P.E, P.in_div, P.R, P.C, P.rows_per_wg, P);                        \
+    else                                                                                                  \
+      KMOE_LAUNCH(name, (tq3_gemv_kernel<CPLV, IN32V, PAIRV, 4>), grid, dim3(256), lds, s, P.w, P.vexp, P.in, \
+                  P.wstride, P.up_off, P.E, P.in_div, P.R, P.C, P.rows_per_wg, P);                        \
   } while (0)
   if (nb > 64) {
     if (pair) KMOE_TQ(2, false, true);
