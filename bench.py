@@ -78,6 +78,8 @@ def parse():
                    help="skip the 4096-token prefill of the hidden-4096 / 512-expert layer")
     p.add_argument("--no-stack60", dest="stack60", action="store_false",
                    help="skip the 60-layer hidden-4096 / 512-expert / top-10 decode stack (~169 GB resident)")
+    p.add_argument("--x-dtype", default="f16", choices=("f16", "bf16", "f32"),
+                   help="activation dtype of the routed-layer cases (the shared-expert layer stays fp16)")
     p.add_argument("--no-tq3", dest="tq3", action="store_false",
                    help="skip the TQ3 codebook expert MLP at 1 and 4 tokens")
     p.add_argument("--no-4bit", dest="four_bit", action="store_false",
@@ -108,6 +110,9 @@ def main():
     from kandiga_amd import synth
     from kandiga_amd.moe import QuantizedExperts, SparseMoeBlock, profile_kernels
 
+    X_DTYPES = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+    XB = {"f16": 2, "bf16": 2, "f32": 4}[args.x_dtype]  # bytes per activation element
+
     dev = torch.device("cuda:0")
     shape = synth.SHAPES["h2048-e256-i512-k8-3bit"]
     H, E, I = shape.hidden, shape.num_experts, shape.intermediate
@@ -127,10 +132,10 @@ def main():
         dn = H * I * shp.bits // 8 + 2 * H * (I // 64) * 2
         act = T * k * I * 4
         if name == "dec_stage1_kernel":
-            return U * gu + T * H * 2 + T * E * 4 + act + T * k * 8
+            return U * gu + T * H * XB + T * E * 4 + act + T * k * 8
         if name == "dec_stage2_kernel":
             return U * dn + act + T * H * 2 + T * k * 8
-        return U * shp.expert_bytes + T * H * 2 + T * E * 4 + T * H * 2 + T * k * 8
+        return U * shp.expert_bytes + T * H * XB + T * E * 4 + T * H * 2 + T * k * 8
 
     def decode_case(T, k, graph, exs=None, shp=None, profile=True, steps=None):
         exs = exs if exs is not None else experts[k]
@@ -147,6 +152,8 @@ def main():
         while p < 64:
             for li, b in enumerate(blocks):
                 x, lg = synth.make_inputs_torch(shp, T, 9000 + 997 * p + 31 * li + T, dev)
+                if not shp.shared_intermediate:  # the dense shared expert takes fp16 x only
+                    x = x.to(X_DTYPES[args.x_dtype])
                 _o, idx, _w = b(x, lg, return_routing=True)
                 ids = torch.unique(idx).tolist()
                 seen[li].update(ids)
@@ -158,7 +165,8 @@ def main():
         P = p
         n = len(seq)
         distinct = sum(len(q) for q in seen) * shp.expert_bytes
-        b_alg = [U * shp.expert_bytes + shp.shared_bytes + T * H * 2 + T * E * 4 + T * H * 2 + T * k * 8
+        xb = 2 if shp.shared_intermediate else XB
+        b_alg = [U * shp.expert_bytes + shp.shared_bytes + T * H * xb + T * E * 4 + T * H * 2 + T * k * 8
                  for U in uniq]
         outs = [None] * n
         if graph:
@@ -257,6 +265,8 @@ def main():
         blk = SparseMoeBlock(ex)
         H, I = shp.hidden, shp.intermediate
         x, lg = synth.make_inputs_torch(shp, T, 12000 + T, dev, zipf=True)
+        if not shp.shared_intermediate:  # the dense shared expert takes fp16 x only
+            x = x.to(X_DTYPES[args.x_dtype])
         ex.reserve(T)
         for _ in range(3):
             blk(x, lg)
@@ -393,7 +403,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u3",
-        "data": "synthetic (seeded MLX-layout 3-bit experts, fp16 scale/bias, fp16 activations; random-init)",
+        "data": "synthetic (seeded MLX-layout 3-bit experts, fp16 scale/bias, %s activations; random-init)"
+                % {"f16": "fp16", "bf16": "bf16", "f32": "fp32"}[args.x_dtype],
         "config": {"workload": "moe-layer decode, %d token%s, 3-bit top-%d, hidden 2048, 256 experts, "
                                "intermediate 512, group 64; stack of %d distinct layers, %d inputs per layer"
                                % (head["T"], "" if head["T"] == 1 else "s", head["k"], args.layers,

@@ -200,10 +200,16 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
     }
   }
   KMOE_MARK(0, 1);
-  // fp16 planes of the activations: as loaded (fp16), or scaled per token (bf16, fp32)
+  // fp16 planes of the activations: as loaded (fp16), or scaled per token (bf16, fp32).  With
+  // scaled activations and routing, the routing wave leaves that work to wave 1, which hands it
+  // the finished planes through LDS behind the barrier: the scaling (a wave max, the split) would
+  // otherwise add to the routing wave's path to the barrier, which every wave waits on.
+  constexpr bool HAND = XS && ROUTE;
+  const bool handed = HAND && wave == 0;
   uint32_t xr[CPL][16], xq[CPL][16];
   float xinv = 1.f, asc = 1.f;  // 2^-s, and 2^2s for act
-  if (!XS) {
+  if (handed) {
+  } else if (!XS) {
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
 #pragma unroll
@@ -231,7 +237,7 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
     const int sx = row_scale_exp(__uint_as_float(wave_max_u32_dpp(__float_as_uint(amax))));
     xinv = exp2i(-sx);
     asc = exp2i(2 * sx);
-    if (lb == 0 && tid == 0 && A.xinv) A.xinv[t] = xinv;
+    if (lb == 0 && wave == (HAND ? 1 : 0) && lane == 0 && A.xinv) A.xinv[t] = xinv;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) split_chunk(v[j], exp2i(sx), xr[j], xq[j]);
   }
@@ -239,6 +245,7 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
   float xs[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
+    if (handed) break;
     to_pair_order<BITS>(xr[j], xp[j]);
     float sm = 0.f;
 #pragma unroll
@@ -260,6 +267,25 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
     for (int m = 0; m < 16; ++m) asm volatile("" : "+v"(xp[j][m]));
     asm volatile("" : "+v"(xs[j]));
   }
+  // lane-major hand-off slots: [chunk][pair word 0..15 | lo word 0..15 | chunk sum][lane]
+  __shared__ uint32_t s_hand[HAND ? CPL * 33 * 64 + 2 : 1];
+  if constexpr (HAND) {
+    if (wave == 1) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+          s_hand[(j * 33 + m) * 64 + lane] = xp[j][m];
+          s_hand[(j * 33 + 16 + m) * 64 + lane] = xlp[j][m];
+        }
+        s_hand[(j * 33 + 32) * 64 + lane] = __float_as_uint(xs[j]);
+      }
+      if (lane == 0) {
+        s_hand[CPL * 33 * 64] = __float_as_uint(xinv);
+        s_hand[CPL * 33 * 64 + 1] = __float_as_uint(asc);
+      }
+    }
+  }
   if constexpr (ROUTE) {
     __syncthreads();
     my = lane < K ? s_sel[lane] : -1;
@@ -267,6 +293,21 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
     if (lane < K) {
       const int e = A.idx_in[t * K + lane];
       my = (e >= 0 && e < E) ? e : -1;
+    }
+  }
+  if constexpr (HAND) {
+    if (handed) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+          xp[j][m] = s_hand[(j * 33 + m) * 64 + lane];
+          xlp[j][m] = s_hand[(j * 33 + 16 + m) * 64 + lane];
+        }
+        xs[j] = __uint_as_float(s_hand[(j * 33 + 32) * 64 + lane]);
+      }
+      xinv = __uint_as_float(s_hand[CPL * 33 * 64]);
+      asc = __uint_as_float(s_hand[CPL * 33 * 64 + 1]);
     }
   }
   KMOE_MARK(0, 2);
@@ -449,6 +490,8 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
     ev1 = idx[lane + 64];
     if (COMBINE) wv1 = wts[lane + 64];
   }
+  // 2^-s of scaled activations, token t in lane t (loaded with the routing, not after the dots)
+  const float xv = xinv && lane < T ? xinv[lane] : 1.f;
   KMOE_MARK(1, 1);
 
   const int LPA = 1 << lpa_log2, AG = 64 >> lpa_log2;
@@ -502,6 +545,7 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
       float part[RPW];
 #pragma unroll
       for (int r = 0; r < RPW; ++r) part[r] = 0.f;
+      const float xq = __shfl(xv, min(U.a, TK - 1) / K, 64);  // every lane: the shuffle is uniform
       if (U.v && cv) {
         float sh = 0.f, sl = 0.f;
 #pragma unroll
@@ -522,7 +566,7 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
       for (int r = 0; r < RPW; ++r) {
         float v = group_sum_last(part[r], LPA);  // 0 for an assignment with an invalid expert
         if (cl == LPA - 1 && u < nunits && U.a < TK) {
-          if (xinv) v *= xinv[U.a / K] * xinv[U.a / K];  // act was stored times 2^2s
+          if (xinv) v *= xq * xq;  // act was stored times 2^2s
           if constexpr (COMBINE) {
             red[U.a * S2_ROWS + (U.hb - h0) + r] = v;
           } else {
@@ -611,11 +655,12 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
 #pragma unroll
       for (int i = 0; i < UF; ++i) {
         const int a = av[i];
+        const float xq = __shfl(xv, min(a, TK - 1) / K, 64);  // every lane: the shuffle is uniform
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
           float v = group_sum_last(part[i][r], LPA);  // 0 for an assignment with an invalid expert
           if (cl == LPA - 1 && u0 + 4 * i < nunits && a < TK) {
-            if (xinv) v *= xinv[a / K] * xinv[a / K];  // act was stored times 2^2s
+            if (xinv) v *= xq * xq;  // act was stored times 2^2s
             if constexpr (COMBINE) {
               red[a * S2_ROWS + (hb[i] - h0) + r] = v;
             } else {
