@@ -425,9 +425,11 @@ int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logi
   if (idx_out) w.idx = idx_out;
   if (weights_out) w.wts = weights_out;
   hipError_t e = hipSuccess;
-  if (a.sh_gate) e = launch_shared(c, static_cast<const uint16_t*>(x), tokens, w, s);
+  const bool decode = is_decode(tokens, K, a.H);
+  // decode runs the dense shared expert inside its two stages
+  if (a.sh_gate && !decode) e = launch_shared(c, static_cast<const uint16_t*>(x), tokens, w, s);
   if (e != hipSuccess) return hip_fail(e, "shared expert launch");
-  if (is_decode(tokens, K, a.H)) {
+  if (decode) {
     DecodeCall d{x, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true, extra, xdt};
     e = launch_decode(c, d, s);
   } else {

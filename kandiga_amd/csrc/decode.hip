@@ -118,7 +118,74 @@ struct Stage1Args {
   float* xinv;              // [T] 2^-s of scaled activations (bf16 / fp32), or null
   int wgs_per_expert;       // row blocks (items) per expert: I / (4*RW)
   int wgs_per_token;        // workgroups working on each token
+  uint16_t* sh_act;         // dense shared expert's SwiGLU output, 2 fp16 planes [T][Is] (or null)
+  size_t sh_plane;          // T*Is
 };
+
+// Rows of the dense fp16 shared expert per wave in the decode stages.
+constexpr int DEC_SH_RW = 2;
+
+// The dense fp16 shared expert's gate/up rows for workgroup b of the workgroups that follow the
+// routed ones in stage 1: DEC_SH_RW gate rows and the same up rows per wave against every
+// token's x (fp16, natural order, read from L2), act = act(g)*u as two fp16 planes.  These rows
+// need no routing, so they stream while the routed workgroups route.  Afterwards the workgroup
+// touches one dword per 128-byte line of its share of the shared down matrix, so stage 2 finds
+// those lines in the caches.
+template <int ACT>
+__device__ __forceinline__ void dec_shared_gateup(const uint16_t* __restrict__ x, int T, int H, const LayerArgs& L,
+                                                  uint16_t* __restrict__ act, size_t plane, int b, int nb) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int i0 = (b * 4 + wave) * DEC_SH_RW;
+  const int nch = H / CHUNK, Is = L.Is;
+  float ag[DEC_SH_RW][DEC_MAX_TOKENS], au[DEC_SH_RW][DEC_MAX_TOKENS];
+#pragma unroll
+  for (int r = 0; r < DEC_SH_RW; ++r)
+#pragma unroll
+    for (int j = 0; j < DEC_MAX_TOKENS; ++j) ag[r][j] = au[r][j] = 0.f;
+  for (int c = lane; c < nch; c += 64) {
+    uint32_t g[DEC_SH_RW][16], u[DEC_SH_RW][16];
+#pragma unroll
+    for (int r = 0; r < DEC_SH_RW; ++r) {
+      load16(L.sh_gate + (size_t)(i0 + r) * H + (size_t)c * CHUNK, g[r]);
+      load16(L.sh_up + (size_t)(i0 + r) * H + (size_t)c * CHUNK, u[r]);
+    }
+#pragma unroll
+    for (int j = 0; j < DEC_MAX_TOKENS; ++j) {
+      if (j < T) {
+        uint32_t xv[16];
+        load16(x + (size_t)j * H + (size_t)c * CHUNK, xv);
+#pragma unroll
+        for (int r = 0; r < DEC_SH_RW; ++r) {
+          ag[r][j] += chunk_dot(g[r], xv);
+          au[r][j] += chunk_dot(u[r], xv);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < DEC_SH_RW; ++r) {
+#pragma unroll
+    for (int j = 0; j < DEC_MAX_TOKENS; ++j) {
+      if (j < T) {
+        const float gs = wave_sum_dpp(ag[r][j]);
+        const float us = wave_sum_dpp(au[r][j]);
+        if (lane == 0) {
+          const float a = activate<ACT>(gs, us);
+          const _Float16 hi = (_Float16)a;
+          const _Float16 lo = (_Float16)(a - (float)hi);
+          const size_t o = (size_t)j * Is + i0 + r;
+          act[o] = __builtin_bit_cast(uint16_t, hi);
+          act[plane + o] = __builtin_bit_cast(uint16_t, lo);
+        }
+      }
+    }
+  }
+  const size_t lines = (size_t)H * Is * 2 / 128;
+  const uint32_t* dn = reinterpret_cast<const uint32_t*>(L.sh_down);
+  uint32_t sink = 0u;
+  for (size_t ln = (size_t)b * 256 + tid; ln < lines; ln += (size_t)nb * 256) sink ^= dn[ln * 32];
+  asm volatile("" ::"v"(sink));
+}
 
 // Stage 1.  Workgroup b works on token t = b / wgs_per_token only: wave 0 routes the token (or
 // every wave reads its given indices) and shares the K experts through LDS behind the kernel's one
@@ -140,11 +207,19 @@ struct Stage1Args {
 // The values the first loads need (logits, x, the sizes) come as leading scalar arguments: gfx950
 // preloads those into SGPRs at wave launch (the library is built with kernel-argument preload),
 // so the x and logits loads issue without waiting for the kernel-argument fetch.
-template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE, bool XS>
+template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE, bool XS, bool SH>
 __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict__ logits,
                                                          const void* __restrict__ x, int H, int E, int K, int I,
-                                                         int wgs_per_token, const Stage1Args A) {
+                                                         int wgs_per_token, int nrouted, const Stage1Args A) {
   const LayerArgs& L = A.L;
+  static_assert(!(SH && XS), "the dense shared expert takes fp16 activations only");
+  if constexpr (SH) {  // workgroups past the routed ones: the dense shared expert's gate/up rows
+    if ((int)blockIdx.x >= nrouted) {
+      dec_shared_gateup<ACT>(static_cast<const uint16_t*>(x), A.T, H, L, A.sh_act, A.sh_plane,
+                             (int)blockIdx.x - nrouted, (int)gridDim.x - nrouted);
+      return;
+    }
+  }
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int nch = H / CHUNK;
   const int t = blockIdx.x / wgs_per_token;
@@ -450,14 +525,15 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
 // have all their loads in flight.  Per-assignment row results go to LDS and the combine
 // sums them in k order (moe_block.metal:515-539), so the result does not depend on timing.
 // The routing pointers and the sizes lead the arguments (preloaded into SGPRs, as for stage 1).
-template <int BITS, bool BF16, int S2_ROWS, int RPW, int UF, bool COMBINE>
+template <int BITS, bool BF16, int S2_ROWS, int RPW, int UF, bool COMBINE, bool SH>
 __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restrict__ idx,
                                                          const float* __restrict__ wts, int T, int K, int TG,
                                                          int lpa_log2, const LayerArgs L,
                                                          const uint16_t* __restrict__ act, size_t act_plane,
                                                          void* __restrict__ out, int out32,
                                                          const float* __restrict__ shared_out,
-                                                         const float* __restrict__ xinv) {
+                                                         const float* __restrict__ xinv,
+                                                         const uint16_t* __restrict__ sh_act, size_t sh_plane) {
   __shared__ float red[DEC_STAGE2_ASSIGN * S2_ROWS];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // Token group blockIdx.y: tokens [t0, t0 + TG) are handled as a call of their own, so a
@@ -473,6 +549,7 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
       out = out32 ? static_cast<void*>(static_cast<float*>(out) + (size_t)t0 * L.H)
                   : static_cast<void*>(static_cast<uint16_t*>(out) + (size_t)t0 * L.H);
       if (shared_out) shared_out += (size_t)t0 * L.H;
+      if constexpr (SH) sh_act += (size_t)t0 * L.Is;
     } else {
       out = static_cast<uint16_t*>(out) + (size_t)t0 * K * L.H;
     }
@@ -673,6 +750,43 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
   }
   KMOE_MARK(1, 2);
   if constexpr (COMBINE) {
+    // The dense fp16 shared expert's down rows of this workgroup (its act came from stage 1's
+    // extra workgroups): LPS lanes per row, every token's act hi + lo planes, results to LDS for
+    // the combine below, which adds them after the routed sum.
+    __shared__ float s_sh[SH ? DEC_MAX_TOKENS * S2_ROWS : 1];
+    if constexpr (SH) {
+      const int nchs = L.Is / CHUNK;
+      int lps = 1;
+      while (lps < nchs && lps < 64) lps <<= 1;
+      const int rpws = 64 / lps, cs = lane & (lps - 1);
+      for (int rb = wave * rpws; rb < S2_ROWS; rb += 4 * rpws) {
+        const int r = rb + lane / lps;
+        float acc[DEC_MAX_TOKENS];
+#pragma unroll
+        for (int j = 0; j < DEC_MAX_TOKENS; ++j) acc[j] = 0.f;
+        if (r < S2_ROWS) {
+          const uint16_t* drow = L.sh_down + (size_t)(h0 + r) * L.Is;
+          for (int c = cs; c < nchs; c += lps) {
+            uint32_t d[16];
+            load16(drow + (size_t)c * CHUNK, d);
+#pragma unroll
+            for (int j = 0; j < DEC_MAX_TOKENS; ++j) {
+              if (j < T) {
+                uint32_t ah[16], al[16];
+                load16(sh_act + (size_t)j * L.Is + (size_t)c * CHUNK, ah);
+                load16(sh_act + sh_plane + (size_t)j * L.Is + (size_t)c * CHUNK, al);
+                acc[j] += chunk_dot(d, ah) + chunk_dot(d, al);
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < DEC_MAX_TOKENS; ++j) {
+          const float v = group_sum_last(acc[j], lps);
+          if (j < T && r < S2_ROWS && cs == lps - 1) s_sh[j * S2_ROWS + r] = v;
+        }
+      }
+    }
     __shared__ float s_wt[DEC_STAGE2_ASSIGN];
     if (wave == 0) {
       if (lane < TK) s_wt[lane] = wv0;
@@ -687,6 +801,7 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
         v = fmaf(s_wt[a], red[a * S2_ROWS + r], v);
       }
       const int h = h0 + r;
+      if constexpr (SH) v += s_sh[t * S2_ROWS + r];
       if (shared_out) v += shared_out[(size_t)t * H + h];
       if (out32)
         static_cast<float*>(out)[(size_t)t * H + h] = v;
@@ -754,8 +869,10 @@ static int lpa_log2_for(int I) {
 
 template <typename KERN>
 static hipError_t launch_stage1(KERN k1, int grid, hipStream_t s, const Stage1Args& A) {
-  KMOE_LAUNCH("dec_stage1_kernel", k1, dim3(grid), dim3(256), 0, s, A.logits, A.x, A.L.H, A.L.E, A.K, A.L.I,
-              A.wgs_per_token, A);
+  // the dense shared expert's gate/up rows (fp16 activations only) as workgroups after the routed ones
+  const int nsh = A.sh_act ? A.L.Is / (4 * DEC_SH_RW) : 0;
+  KMOE_LAUNCH("dec_stage1_kernel", k1, dim3(grid + nsh), dim3(256), 0, s, A.logits, A.x, A.L.H, A.L.E, A.K,
+              A.L.I, A.wgs_per_token, grid, A);
   return hipGetLastError();
 }
 
@@ -781,6 +898,8 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   A.act = w.act;
   A.act_plane = (size_t)T * K * L.I;
   A.xinv = d.xdt == XDT_F16 ? nullptr : w.xinv;
+  A.sh_act = L.sh_gate && d.xdt == XDT_F16 ? w.shared_act : nullptr;
+  A.sh_plane = (size_t)T * L.Is;
   A.wgs_per_expert = L.I / (4 * RW);
   // at most two workgroups per CU in all: every workgroup repeats its token's routing, so the
   // grid stays resident and loops over the token's (expert, row block) items instead
@@ -789,11 +908,20 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   hipError_t err;
   auto stage1 = [&](auto xs) {
     constexpr bool XSV = decltype(xs)::value;
+    if constexpr (!XSV) {  // the dense shared expert's gate/up rows ride along (fp16 activations)
+      if (A.sh_act) {
+        if (nch <= 64)
+          return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, false, true>, grid1, s, A)
+                          : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, false, true>, grid1, s, A);
+        return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, false, true>, grid1, s, A)
+                        : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, false, true>, grid1, s, A);
+      }
+    }
     if (nch <= 64)
-      return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, XSV>, grid1, s, A)
-                      : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, XSV>, grid1, s, A);
-    return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, XSV>, grid1, s, A)
-                    : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, XSV>, grid1, s, A);
+      return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, XSV, false>, grid1, s, A)
+                      : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, XSV, false>, grid1, s, A);
+    return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, XSV, false>, grid1, s, A)
+                    : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, XSV, false>, grid1, s, A);
   };
   err = d.xdt == XDT_F16 ? stage1(std::false_type{}) : stage1(std::true_type{});
   if (err != hipSuccess) return err;
@@ -805,17 +933,25 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   // 8 assignments per workgroup.  Below 32 assignments short row blocks over all tokens are
   // faster.
   const int32_t* idx = d.idx_in ? d.idx_in : d.idx_out;
-  const float* sho = d.extra ? d.extra : L.sh_gate ? (const float*)w.shared_out : (const float*)nullptr;
+  // the dense shared expert runs inside the two stages (fp16 activations, the only ones it takes)
+  uint16_t* const sh_act = L.sh_gate && d.xdt == XDT_F16 ? w.shared_act : nullptr;
+  const size_t sh_plane = (size_t)T * L.Is;
+  const float* sho = d.extra;
   auto stage2 = [&](auto srows, auto rpw, int TG) {
     constexpr int SR = decltype(srows)::value, RP = decltype(rpw)::value, UF = 2;
     const dim3 grid2(L.H / SR, (T + TG - 1) / TG);
-    if (d.combine) {
-      KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, true>), grid2, dim3(256), 0, s, idx,
-                  d.wts, T, K, TG, l2, L, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, A.xinv);
+    if (d.combine && sh_act) {
+      KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, true, true>), grid2, dim3(256), 0, s,
+                  idx, d.wts, T, K, TG, l2, L, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, A.xinv,
+                  (const uint16_t*)sh_act, sh_plane);
+    } else if (d.combine) {
+      KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, true, false>), grid2, dim3(256), 0, s,
+                  idx, d.wts, T, K, TG, l2, L, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, A.xinv,
+                  (const uint16_t*)nullptr, (size_t)0);
     } else {
-      KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, false>), grid2, dim3(256), 0, s,
+      KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, false, false>), grid2, dim3(256), 0, s,
                   idx, (const float*)nullptr, T, K, TG, l2, L, (const uint16_t*)w.act, A.act_plane, d.out, 0,
-                  (const float*)nullptr, A.xinv);
+                  (const float*)nullptr, A.xinv, (const uint16_t*)nullptr, (size_t)0);
     }
   };
   using I4 = std::integral_constant<int, 4>;
