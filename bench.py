@@ -80,6 +80,8 @@ def parse():
                    help="skip the 60-layer hidden-4096 / 512-expert / top-10 decode stack (~169 GB resident)")
     p.add_argument("--x-dtype", default="f16", choices=("f16", "bf16", "f32"),
                    help="activation dtype of the routed-layer cases (the shared-expert layer stays fp16)")
+    p.add_argument("--no-block", dest="block", action="store_false",
+                   help="skip the whole-block decode (router, routed experts, gated shared expert, residual)")
     p.add_argument("--no-tq3", dest="tq3", action="store_false",
                    help="skip the TQ3 codebook expert MLP at 1 and 4 tokens")
     p.add_argument("--no-4bit", dest="four_bit", action="store_false",
@@ -301,6 +303,11 @@ def main():
             prefill[f"prefill_copy_T{T}"] = prefill_case(ex_pk, shape, T, " (prefill copy)")
         del ex_pk
 
+    # the whole MoE block (router projection, routed experts, gated shared expert, residual) on the
+    # same 8 resident layers, decode over enough inputs that a replay touches >= 1 GiB of experts
+    if args.block and args.decode:
+        results.update(block_cases(torch, dev, shape, experts[8], args.steps, log))
+
     # the hidden-2560 layer with a dense fp16 shared expert (decode over 4 rotated layers)
     if args.shared_layer:
         shp4 = synth.SHAPES["h2560-e256-i1024-k8-3bit-shared1024"]
@@ -422,6 +429,66 @@ def main():
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def block_cases(torch, dev, shape, layers, steps, log) -> dict:
+    """The whole MoE block of a Qwen-style layer (kmoe_block_forward) at 1 and 8 tokens: a 4-bit
+    bf16-scale router projection [256, 2048] and shared expert (intermediate 512, sigmoid gate)
+    around each of the resident 3-bit routed layers, a residual, fp16 out.  Graph replay over
+    enough token inputs per layer that a replay touches >= 1 GiB of distinct routed experts;
+    GB/s counts the distinct routed experts, the router, shared expert and gate bytes, x,
+    residual and out."""
+    from kandiga_amd import synth
+    from kandiga_amd.moe import MoEBlock
+
+    H, E, K, Is = shape.hidden, shape.num_experts, shape.top_k, 512
+    blocks = [MoEBlock.from_arrays(ex, synth.make_block(shape, Is, 8300 + i, bits=4, scale_dtype="bf16"), 4, "bf16")
+              for i, ex in enumerate(layers)]
+    q4 = lambda rows, cols: rows * cols // 2 + 2 * rows * (cols // 64) * 2  # 4-bit codes + bf16 s, b
+    extra = q4(E, H) + 2 * q4(Is, H) + q4(H, Is) + q4(1, H)
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(8400)
+    for T in (1, 8):
+        seq, seen, uniq = [], [set() for _ in blocks], []
+        p = 0
+        while p < 64:
+            for li, b in enumerate(blocks):
+                b.workspace(T)
+                x = torch.randn((T, H), device=dev, generator=g).half()
+                res = torch.randn((T, H), device=dev, generator=g).half()
+                _o, idx, _w, _lg = b(x, res, return_routing=True)
+                ids = torch.unique(idx).tolist()
+                seen[li].update(ids)
+                uniq.append(len(ids))
+                seq.append((b, x, res))
+            p += 1
+            if sum(len(q) for q in seen) * shape.expert_bytes >= 2 ** 30:
+                break
+        n = len(seq)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for b, x, res in seq:
+                b(x, res)
+        reps = max(5, -(-steps // n))
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * n)
+        U = sum(uniq) / n
+        ba = U * shape.expert_bytes + extra + 3 * T * H * 2
+        out[f"block_decode_T{T}_K{K}_graph"] = {"T": T, "k": K, "us_per_layer": us, "gbs": ba / (us * 1e-6) / 1e9,
+                                                "bytes_alg": ba, "unique_experts": U, "calls": reps * n,
+                                                "inputs_per_layer": p, "shared_intermediate": Is}
+        log(f"MoE block decode T={T}: {us:.2f} us/layer  {ba / (us * 1e-6) / 1e9:.0f} GB/s  U={U:.1f} P={p}")
+    del blocks
+    return out
 
 
 def tq3_cases(torch, dev, shape, steps, profile_kernels, log) -> dict:

@@ -13,6 +13,8 @@
 //     term the routed layer's combine adds after the weighted expert sum (moe_block.metal:
 //     556-584 keeps the shared output in fp16 and gates it in fp32).
 //   fill_i32_kernel: the expert index 0 of every token for the one-expert shared layer.
+#include <mutex>
+
 #include "kmoe_device.h"
 #include "kmoe_internal.h"
 
@@ -95,6 +97,24 @@ __global__ __launch_bounds__(256) void blend_prep_kernel(const uint16_t* __restr
 __global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* __restrict__ p, int n, int32_t v) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i < n) p[i] = v;
+}
+
+// Never written: the loader places it, zeroed, on every device the library runs on.
+__device__ int32_t g_zero_index[DEC_MAX_TOKENS] = {};
+
+const int32_t* zero_index() {
+  constexpr int kMaxDev = 64;
+  static std::mutex mu;
+  static const int32_t* ptr[kMaxDev] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_zero_index)) != hipSuccess) return nullptr;
+    ptr[dev] = static_cast<const int32_t*>(p);
+  }
+  return ptr[dev];
 }
 
 hipError_t launch_qlinear(const QProj& a, int ra, const QProj& b, int rb, int bits, bool bf16, const uint16_t* x,

@@ -402,7 +402,7 @@ int kmoe_forward_x(const kmoe_layer* layer, const void* x, int32_t x_dtype, cons
 // library's static scratch).
 int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                        int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace,
-                       size_t workspace_bytes, void* stream, const float* extra, int xdt) {
+                       size_t workspace_bytes, void* stream, const float* extra, int xdt, const Blend* blend) {
   if (!layer) return fail(KMOE_ERR_INVALID_ARG, "null layer");
   if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
   if (out_dtype != KMOE_OUT_F16 && out_dtype != KMOE_OUT_F32) return fail(KMOE_ERR_INVALID_ARG, "unknown out_dtype");
@@ -431,6 +431,7 @@ int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logi
   if (e != hipSuccess) return hip_fail(e, "shared expert launch");
   if (decode) {
     DecodeCall d{x, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true, extra, xdt};
+    if (blend) d.blend = *blend;
     e = launch_decode(c, d, s);
   } else {
     const int bm = gemm_bm(a, xdt), mmt = max_mtiles_for(tokens * K, a.E, bm);
@@ -733,10 +734,13 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
   hipError_t e = launch_qlinear(block->router, ra.E, block->sgate, block->gated ? 1 : 0, block->bits, block->bf16, xx,
                                 tokens, ra.H, logits, w.gate, s);
   if (e == hipSuccess && block->has_shared) {
-    e = launch_fill_i32(w.idx0, tokens, 0, s);
     const LayerConfig& sc = block->shared;
+    // expert index 0 of every token for the one-expert shared layer: the library's constant zeros
+    // in decode, else filled into the workspace
+    const int32_t* zi = is_decode(tokens, 1, ra.H) ? zero_index() : nullptr;
+    if (!zi) e = launch_fill_i32(w.idx0, tokens, 0, s);
     if (e == hipSuccess && is_decode(tokens, 1, ra.H)) {
-      DecodeCall d{xx, nullptr, w.idx0, tokens, nullptr, nullptr, nullptr, &w.sh, w.ysh, 0, false, nullptr};
+      DecodeCall d{xx, nullptr, zi ? zi : w.idx0, tokens, nullptr, nullptr, nullptr, &w.sh, w.ysh, 0, false, nullptr};
       e = launch_decode(sc, d, s);
     } else if (e == hipSuccess) {
       const int bm = gemm_bm(sc.args), mmt = max_mtiles_for(tokens, 1, bm);
@@ -746,12 +750,21 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
     }
   }
   const bool need_extra = block->has_shared || residual;
-  if (e == hipSuccess && need_extra)
+  // decode adds residual + fp16 shared * sigmoid(gate) inside its combine; prefill's combine adds
+  // the fp32 term prepared here
+  const bool fused = is_decode(tokens, block->routed->cfg.top_k, ra.H);
+  Blend bl;
+  if (fused) {
+    bl.res = static_cast<const uint16_t*>(residual);
+    bl.sh = block->has_shared ? w.ysh : nullptr;
+    bl.gate = block->has_shared && block->gated ? w.gate : nullptr;
+  } else if (e == hipSuccess && need_extra) {
     e = launch_blend_prep(block->has_shared ? w.ysh : nullptr, block->gated ? w.gate : nullptr,
                           static_cast<const uint16_t*>(residual), tokens, ra.H, w.extra, s);
+  }
   if (e != hipSuccess) return hip_fail(e, "block launch");
   return kmoe::forward_impl(block->routed, x, logits, tokens, out, out_dtype, idx_out, weights_out, w.routed,
-                            w.routed_bytes, stream, need_extra ? w.extra : nullptr);
+                            w.routed_bytes, stream, !fused && need_extra ? w.extra : nullptr, KMOE_X_F16, &bl);
 }
 
 }  // extern "C"

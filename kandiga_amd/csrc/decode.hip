@@ -533,7 +533,8 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
                                                          void* __restrict__ out, int out32,
                                                          const float* __restrict__ shared_out,
                                                          const float* __restrict__ xinv,
-                                                         const uint16_t* __restrict__ sh_act, size_t sh_plane) {
+                                                         const uint16_t* __restrict__ sh_act, size_t sh_plane,
+                                                         Blend B) {
   __shared__ float red[DEC_STAGE2_ASSIGN * S2_ROWS];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // Token group blockIdx.y: tokens [t0, t0 + TG) are handled as a call of their own, so a
@@ -549,6 +550,9 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
       out = out32 ? static_cast<void*>(static_cast<float*>(out) + (size_t)t0 * L.H)
                   : static_cast<void*>(static_cast<uint16_t*>(out) + (size_t)t0 * L.H);
       if (shared_out) shared_out += (size_t)t0 * L.H;
+      if (B.res) B.res += (size_t)t0 * L.H;
+      if (B.sh) B.sh += (size_t)t0 * L.H;
+      if (B.gate) B.gate += t0;
       if constexpr (SH) sh_act += (size_t)t0 * L.Is;
     } else {
       out = static_cast<uint16_t*>(out) + (size_t)t0 * K * L.H;
@@ -569,6 +573,20 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
   }
   // 2^-s of scaled activations, token t in lane t (loaded with the routing, not after the dots)
   const float xv = xinv && lane < T ? xinv[lane] : 1.f;
+  // the term this thread's combine output adds after the routed sum, loaded now rather than
+  // after the dots: the fp32 extra row, or the block's residual + fp16 shared * sigmoid(gate)
+  const bool add_term = COMBINE && (shared_out || B.res || B.sh);
+  float term = 0.f;
+  if (add_term && tid < T * S2_ROWS) {
+    const int tt = tid / S2_ROWS, hh = blockIdx.x * S2_ROWS + (tid - tt * S2_ROWS);
+    const size_t o = (size_t)tt * L.H + hh;
+    if (shared_out) {
+      term = shared_out[o];
+    } else {
+      term = B.res ? f16_bits_to_f32(B.res[o]) : 0.f;
+      if (B.sh) term += f16_bits_to_f32(B.sh[o]) * (B.gate ? 1.0f / (1.0f + expf(-B.gate[tt])) : 1.0f);
+    }
+  }
   KMOE_MARK(1, 1);
 
   const int LPA = 1 << lpa_log2, AG = 64 >> lpa_log2;
@@ -802,7 +820,7 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
       }
       const int h = h0 + r;
       if constexpr (SH) v += s_sh[t * S2_ROWS + r];
-      if (shared_out) v += shared_out[(size_t)t * H + h];
+      if (add_term) v += term;
       if (out32)
         static_cast<float*>(out)[(size_t)t * H + h] = v;
       else
@@ -943,15 +961,15 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
     if (d.combine && sh_act) {
       KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, true, true>), grid2, dim3(256), 0, s,
                   idx, d.wts, T, K, TG, l2, L, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, A.xinv,
-                  (const uint16_t*)sh_act, sh_plane);
+                  (const uint16_t*)sh_act, sh_plane, d.blend);
     } else if (d.combine) {
       KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, true, false>), grid2, dim3(256), 0, s,
                   idx, d.wts, T, K, TG, l2, L, (const uint16_t*)w.act, A.act_plane, d.out, d.out32, sho, A.xinv,
-                  (const uint16_t*)nullptr, (size_t)0);
+                  (const uint16_t*)nullptr, (size_t)0, d.blend);
     } else {
       KMOE_LAUNCH("dec_stage2_kernel", (dec_stage2_kernel<BITS, BF16, SR, RP, UF, false, false>), grid2, dim3(256), 0, s,
                   idx, (const float*)nullptr, T, K, TG, l2, L, (const uint16_t*)w.act, A.act_plane, d.out, 0,
-                  (const float*)nullptr, A.xinv, (const uint16_t*)nullptr, (size_t)0);
+                  (const float*)nullptr, A.xinv, (const uint16_t*)nullptr, (size_t)0, Blend{});
     }
   };
   using I4 = std::integral_constant<int, 4>;

@@ -91,6 +91,15 @@ constexpr int DEVERR_BAD_EXPERT = 1;
 constexpr int XDT_F16 = 0, XDT_BF16 = 1, XDT_F32 = 2;
 
 // One decode-path call (1..DEC_MAX_TOKENS tokens): routing from logits, or given indices.
+// The MoE block's term after the routed combine, out = routed + (residual + fp16 shared * gate'):
+// res [T][H] fp16 or null, sh [T][H] fp16 (the block's shared-expert output) or null, gate [T]
+// fp32 pre-sigmoid or null (ungated).  Decode adds it inside its combine.
+struct Blend {
+  const uint16_t* res = nullptr;
+  const uint16_t* sh = nullptr;
+  const float* gate = nullptr;
+};
+
 struct DecodeCall {
   const void* x;           // [T][H] of dtype xdt
   const float* logits;     // [T][E], or null when idx_in is given
@@ -106,6 +115,7 @@ struct DecodeCall {
   const float* extra;      // [T][H] fp32 added after the combine (block residual + gated shared
                            // expert), or null: then the layer's dense shared expert output, if any
   int xdt;                 // XDT_* of x
+  Blend blend;             // block term added in the combine (decode only)
 };
 
 // Kernel timing hook (kmoe_profile_begin/end).  prof_events hands out the next event pair of
@@ -134,7 +144,7 @@ namespace kmoe {
 // those of kmoe_forward.
 int forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                  int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
-                 void* stream, const float* extra = nullptr, int xdt = XDT_F16);
+                 void* stream, const float* extra = nullptr, int xdt = XDT_F16, const Blend* blend = nullptr);
 // kmoe_workspace_size for `tokens` tokens of `layer`.
 int workspace_bytes_for(const kmoe_layer* layer, int32_t tokens, size_t* bytes);
 // Records `msg` as the calling thread's last error and returns `code`.
@@ -179,6 +189,9 @@ hipError_t launch_qlinear(const QProj& a, int ra, const QProj& b, int rb, int bi
 hipError_t launch_blend_prep(const uint16_t* shared16, const float* gate, const uint16_t* residual, int T, int H,
                              float* extra, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t s);
+// DEC_MAX_TOKENS constant zeros in device memory of the current device (expert index 0 of every
+// token of a one-expert layer in decode), or null if its address could not be obtained.
+const int32_t* zero_index();
 // TQ3 GEMV (tq3.hip): out[v][r] = row r of the TQ3 matrix of expert vexp[v] (at w + e * wstride;
 // null vexp: expert 0) dotted with input row v / in_div (fp16, or fp32 when in32; rotated by the
 // kernel); pair: r indexes gate/up row pairs (up matrix at + up_off) and out = silu(gate) * up.
