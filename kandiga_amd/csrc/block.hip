@@ -17,66 +17,15 @@
 
 #include "kmoe_device.h"
 #include "kmoe_internal.h"
+#include "qlinear.h"
 
 namespace kmoe {
-
-constexpr int QL_TB = 4;    // tokens per workgroup
-constexpr int QL_RPW = 2;   // rows per wave
-constexpr uint32_t QL_ONE2 = 0x3C003C00u;
-constexpr float QL_TWO24 = 16777216.0f;
 
 template <int BITS, bool BF16>
 __global__ __launch_bounds__(256) void qlinear_kernel(const QProj A, int ra, const QProj B, int rb, int T, int H,
                                                       const uint16_t* __restrict__ x, float* __restrict__ out_a,
                                                       float* __restrict__ out_b) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int R = ra + rb;
-  const int t0 = blockIdx.y * QL_TB;
-  const int r0 = (blockIdx.x * 4 + wave) * QL_RPW;
-  const int nch = H / CHUNK, ng = H / GROUP;
-  const size_t rbytes = (size_t)H * BITS / 8;
-  float acc[QL_RPW * QL_TB];
-#pragma unroll
-  for (int v = 0; v < QL_RPW * QL_TB; ++v) acc[v] = 0.f;
-  for (int c = lane; c < nch; c += 64) {
-    uint32_t xp[QL_TB][16];
-    float xs[QL_TB];
-#pragma unroll
-    for (int t = 0; t < QL_TB; ++t) {
-      uint32_t nat[16];
-      const int tt = min(t0 + t, T - 1);  // tokens past T reload the last one (never stored)
-      load16g(x + (size_t)tt * H + (size_t)c * CHUNK, nat);
-      float sm = 0.f;
-#pragma unroll
-      for (int m = 0; m < 16; ++m) sm = fdot2(nat[m], QL_ONE2, sm);
-      xs[t] = sm;
-      to_pair_order<BITS>(nat, xp[t]);
-    }
-#pragma unroll
-    for (int r = 0; r < QL_RPW; ++r) {
-      const int row = min(r0 + r, R - 1);  // rows past R recompute the last one (never stored)
-      const QProj& P = row < ra ? A : B;
-      const int pr = row < ra ? row : row - ra;
-      uint32_t d[4], cp[16];
-      load_chunk<BITS>(P.w + (size_t)pr * rbytes, c, d);
-      unpack_chunk<BITS, false>(d, cp);
-      const float sf = scale_to_f32<BF16>(P.s[(size_t)pr * ng + (c >> 1)]) * QL_TWO24;
-      const float bf = scale_to_f32<BF16>(P.b[(size_t)pr * ng + (c >> 1)]);
-#pragma unroll
-      for (int t = 0; t < QL_TB; ++t) acc[r * QL_TB + t] += sf * chunk_dot(cp, xp[t]) + bf * xs[t];
-    }
-  }
-  const float tot = wave_sum_multi<8>(acc);  // value v = r*QL_TB + t lands in lanes 8v..8v+7
-  if ((lane & 7) == 0) {
-    const int v = lane >> 3, r = v / QL_TB, t = v - r * QL_TB;
-    const int row = r0 + r, tok = t0 + t;
-    if (row < R && tok < T) {
-      if (row < ra)
-        out_a[(size_t)tok * ra + row] = tot;
-      else
-        out_b[(size_t)tok * rb + (row - ra)] = tot;
-    }
-  }
+  qlinear_rows<BITS, BF16>(A, ra, B, rb, T, H, x, out_a, out_b, (int)blockIdx.x, (int)blockIdx.y);
 }
 
 __global__ __launch_bounds__(256) void blend_prep_kernel(const uint16_t* __restrict__ shared16,
@@ -121,7 +70,7 @@ hipError_t launch_qlinear(const QProj& a, int ra, const QProj& b, int rb, int bi
                           int T, int H, float* out_a, float* out_b, hipStream_t s) {
   const int R = ra + rb;
   if (T == 0 || R == 0) return hipSuccess;
-  const dim3 grid((R + 4 * QL_RPW - 1) / (4 * QL_RPW), (T + QL_TB - 1) / QL_TB);
+  const dim3 grid(qlinear_row_blocks(R), qlinear_token_blocks(T));
 #define KMOE_QL(BB, FF) \
   KMOE_LAUNCH("qlinear_kernel", (qlinear_kernel<BB, FF>), grid, dim3(256), 0, s, a, ra, b, rb, T, H, x, out_a, out_b)
   if (bits == 3) {

@@ -731,8 +731,21 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
   const LayerArgs& ra = block->routed->cfg.args;
   const uint16_t* xx = static_cast<const uint16_t*>(x);
   float* logits = logits_out ? logits_out : w.logits;
-  hipError_t e = launch_qlinear(block->router, ra.E, block->sgate, block->gated ? 1 : 0, block->bits, block->bf16, xx,
-                                tokens, ra.H, logits, w.gate, s);
+  // In decode the router projection rides along the shared layer's stage 1 as extra workgroups
+  // (same bits and scale dtype); otherwise it is a launch of its own.
+  const bool ql_ride = block->has_shared && is_decode(tokens, 1, ra.H) && block->shared.bits == block->bits &&
+                       (block->shared.bf16_scales != 0) == (block->bf16 != 0);
+  QLin ql;
+  ql.a = block->router;
+  ql.ra = ra.E;
+  ql.b = block->sgate;
+  ql.rb = block->gated ? 1 : 0;
+  ql.out_a = logits;
+  ql.out_b = w.gate;
+  hipError_t e = hipSuccess;
+  if (!ql_ride)
+    e = launch_qlinear(block->router, ra.E, block->sgate, block->gated ? 1 : 0, block->bits, block->bf16, xx, tokens,
+                       ra.H, logits, w.gate, s);
   if (e == hipSuccess && block->has_shared) {
     const LayerConfig& sc = block->shared;
     // expert index 0 of every token for the one-expert shared layer: the library's constant zeros
@@ -741,6 +754,7 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
     if (!zi) e = launch_fill_i32(w.idx0, tokens, 0, s);
     if (e == hipSuccess && is_decode(tokens, 1, ra.H)) {
       DecodeCall d{xx, nullptr, zi ? zi : w.idx0, tokens, nullptr, nullptr, nullptr, &w.sh, w.ysh, 0, false, nullptr};
+      if (ql_ride) d.ql = &ql;
       e = launch_decode(sc, d, s);
     } else if (e == hipSuccess) {
       const int bm = gemm_bm(sc.args), mmt = max_mtiles_for(tokens, 1, bm);

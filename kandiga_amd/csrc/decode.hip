@@ -30,6 +30,7 @@
 
 #include "kmoe_device.h"
 #include "kmoe_internal.h"
+#include "qlinear.h"
 
 #include <type_traits>
 
@@ -120,6 +121,8 @@ struct Stage1Args {
   int wgs_per_token;        // workgroups working on each token
   uint16_t* sh_act;         // dense shared expert's SwiGLU output, 2 fp16 planes [T][Is] (or null)
   size_t sh_plane;          // T*Is
+  QLin ql;                  // router projection of extra workgroups (QL instantiations)
+  int ql_row_blocks;        // its workgroups: row blocks x token blocks
 };
 
 // Rows of the dense fp16 shared expert per wave in the decode stages.
@@ -207,12 +210,21 @@ __device__ __forceinline__ void dec_shared_gateup(const uint16_t* __restrict__ x
 // The values the first loads need (logits, x, the sizes) come as leading scalar arguments: gfx950
 // preloads those into SGPRs at wave launch (the library is built with kernel-argument preload),
 // so the x and logits loads issue without waiting for the kernel-argument fetch.
-template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE, bool XS, bool SH>
+template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE, bool XS, bool SH, bool QL>
 __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict__ logits,
                                                          const void* __restrict__ x, int H, int E, int K, int I,
                                                          int wgs_per_token, int nrouted, const Stage1Args A) {
   const LayerArgs& L = A.L;
   static_assert(!(SH && XS), "the dense shared expert takes fp16 activations only");
+  static_assert(!(QL && (XS || SH || ROUTE)), "the router projection rides along the block's shared layer only");
+  if constexpr (QL) {  // workgroups past the shared layer's: the block's router projection
+    if ((int)blockIdx.x >= nrouted) {
+      const int bid = (int)blockIdx.x - nrouted;
+      qlinear_rows<BITS, BF16>(A.ql.a, A.ql.ra, A.ql.b, A.ql.rb, A.T, H, static_cast<const uint16_t*>(x), A.ql.out_a,
+                               A.ql.out_b, bid % A.ql_row_blocks, bid / A.ql_row_blocks);
+      return;
+    }
+  }
   if constexpr (SH) {  // workgroups past the routed ones: the dense shared expert's gate/up rows
     if ((int)blockIdx.x >= nrouted) {
       dec_shared_gateup<ACT>(static_cast<const uint16_t*>(x), A.T, H, L, A.sh_act, A.sh_plane,
@@ -887,8 +899,10 @@ static int lpa_log2_for(int I) {
 
 template <typename KERN>
 static hipError_t launch_stage1(KERN k1, int grid, hipStream_t s, const Stage1Args& A) {
-  // the dense shared expert's gate/up rows (fp16 activations only) as workgroups after the routed ones
-  const int nsh = A.sh_act ? A.L.Is / (4 * DEC_SH_RW) : 0;
+  // extra workgroups after the routed ones: the dense shared expert's gate/up rows (fp16
+  // activations only) or the block's router projection
+  const int nsh = A.sh_act ? A.L.Is / (4 * DEC_SH_RW)
+                 : A.ql.out_a ? A.ql_row_blocks * qlinear_token_blocks(A.T) : 0;
   KMOE_LAUNCH("dec_stage1_kernel", k1, dim3(grid + nsh), dim3(256), 0, s, A.logits, A.x, A.L.H, A.L.E, A.K,
               A.L.I, A.wgs_per_token, grid, A);
   return hipGetLastError();
@@ -918,6 +932,9 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   A.xinv = d.xdt == XDT_F16 ? nullptr : w.xinv;
   A.sh_act = L.sh_gate && d.xdt == XDT_F16 ? w.shared_act : nullptr;
   A.sh_plane = (size_t)T * L.Is;
+  A.ql = d.ql ? *d.ql : QLin{};
+  A.ql_row_blocks = qlinear_row_blocks(A.ql.ra + A.ql.rb);
+  if (d.ql && (d.logits || d.xdt != XDT_F16)) return hipErrorInvalidValue;
   A.wgs_per_expert = L.I / (4 * RW);
   // at most two workgroups per CU in all: every workgroup repeats its token's routing, so the
   // grid stays resident and loops over the token's (expert, row block) items instead
@@ -926,20 +943,26 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   hipError_t err;
   auto stage1 = [&](auto xs) {
     constexpr bool XSV = decltype(xs)::value;
-    if constexpr (!XSV) {  // the dense shared expert's gate/up rows ride along (fp16 activations)
+    if constexpr (!XSV) {
+      if (A.ql.out_a) {  // the block's router projection rides along (given indices, fp16)
+        if (nch <= 64)
+          return launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, false, false, true>, grid1, s, A);
+        return launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, false, false, true>, grid1, s, A);
+      }
+      // the dense shared expert's gate/up rows ride along (fp16 activations)
       if (A.sh_act) {
         if (nch <= 64)
-          return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, false, true>, grid1, s, A)
-                          : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, false, true>, grid1, s, A);
-        return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, false, true>, grid1, s, A)
-                        : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, false, true>, grid1, s, A);
+          return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, false, true, false>, grid1, s, A)
+                          : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, false, true, false>, grid1, s, A);
+        return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, false, true, false>, grid1, s, A)
+                        : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, false, true, false>, grid1, s, A);
       }
     }
     if (nch <= 64)
-      return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, XSV, false>, grid1, s, A)
-                      : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, XSV, false>, grid1, s, A);
-    return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, XSV, false>, grid1, s, A)
-                    : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, XSV, false>, grid1, s, A);
+      return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, XSV, false, false>, grid1, s, A)
+                      : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, XSV, false, false>, grid1, s, A);
+    return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, XSV, false, false>, grid1, s, A)
+                    : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, XSV, false, false>, grid1, s, A);
   };
   err = d.xdt == XDT_F16 ? stage1(std::false_type{}) : stage1(std::true_type{});
   if (err != hipSuccess) return err;

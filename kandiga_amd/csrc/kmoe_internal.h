@@ -100,6 +100,15 @@ struct Blend {
   const float* gate = nullptr;
 };
 
+// A router projection (qlinear_kernel's work: out_a [T][ra] = A x, out_b [T][rb] = B x) run by
+// extra workgroups of a decode stage 1 that takes given indices (the MoE block's shared layer).
+struct QLin {
+  QProj a, b;
+  int ra = 0, rb = 0;
+  float* out_a = nullptr;
+  float* out_b = nullptr;
+};
+
 struct DecodeCall {
   const void* x;           // [T][H] of dtype xdt
   const float* logits;     // [T][E], or null when idx_in is given
@@ -116,6 +125,7 @@ struct DecodeCall {
                            // expert), or null: then the layer's dense shared expert output, if any
   int xdt;                 // XDT_* of x
   Blend blend;             // block term added in the combine (decode only)
+  const QLin* ql = nullptr; // router projection riding along stage 1 (given-indices mode only)
 };
 
 // Kernel timing hook (kmoe_profile_begin/end).  prof_events hands out the next event pair of
