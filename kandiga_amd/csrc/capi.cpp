@@ -402,7 +402,8 @@ int kmoe_forward_x(const kmoe_layer* layer, const void* x, int32_t x_dtype, cons
 // library's static scratch).
 int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                        int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace,
-                       size_t workspace_bytes, void* stream, const float* extra, int xdt, const Blend* blend) {
+                       size_t workspace_bytes, void* stream, const float* extra, int xdt, const Blend* blend,
+                       const QDown* qd) {
   if (!layer) return fail(KMOE_ERR_INVALID_ARG, "null layer");
   if (tokens < 0) return fail(KMOE_ERR_INVALID_ARG, "tokens must be >= 0");
   if (out_dtype != KMOE_OUT_F16 && out_dtype != KMOE_OUT_F32) return fail(KMOE_ERR_INVALID_ARG, "unknown out_dtype");
@@ -432,6 +433,7 @@ int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logi
   if (decode) {
     DecodeCall d{x, logits, nullptr, tokens, w.idx, w.wts, w.wts, &w, out, out32, true, extra, xdt};
     if (blend) d.blend = *blend;
+    d.qd = qd;
     e = launch_decode(c, d, s);
   } else {
     const int bm = gemm_bm(a, xdt), mmt = max_mtiles_for(tokens * K, a.E, bm);
@@ -735,6 +737,19 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
   // (same bits and scale dtype); otherwise it is a launch of its own.
   const bool ql_ride = block->has_shared && is_decode(tokens, 1, ra.H) && block->shared.bits == block->bits &&
                        (block->shared.bf16_scales != 0) == (block->bf16 != 0);
+  // ... and the shared expert's down rows ride along the routed layer's stage 1 (its stage-1 act
+  // being ready by then), so decode makes three launches
+  const bool qd_ride = ql_ride && is_decode(tokens, block->routed->cfg.top_k, ra.H);
+  QDown qd;
+  if (qd_ride) {
+    qd.d = block->shared.args.down;
+    qd.bits = block->shared.bits;
+    qd.bf16 = block->shared.bf16_scales;
+    qd.I = block->shared.args.I;
+    qd.act = w.sh.act;
+    qd.plane = (size_t)tokens * block->shared.args.I;
+    qd.y = w.ysh;
+  }
   QLin ql;
   ql.a = block->router;
   ql.ra = ra.E;
@@ -755,6 +770,7 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
     if (e == hipSuccess && is_decode(tokens, 1, ra.H)) {
       DecodeCall d{xx, nullptr, zi ? zi : w.idx0, tokens, nullptr, nullptr, nullptr, &w.sh, w.ysh, 0, false, nullptr};
       if (ql_ride) d.ql = &ql;
+      d.stage1_only = qd_ride;  // its down rows ride along the routed layer's stage 1
       e = launch_decode(sc, d, s);
     } else if (e == hipSuccess) {
       const int bm = gemm_bm(sc.args), mmt = max_mtiles_for(tokens, 1, bm);
@@ -778,7 +794,8 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
   }
   if (e != hipSuccess) return hip_fail(e, "block launch");
   return kmoe::forward_impl(block->routed, x, logits, tokens, out, out_dtype, idx_out, weights_out, w.routed,
-                            w.routed_bytes, stream, !fused && need_extra ? w.extra : nullptr, KMOE_X_F16, &bl);
+                            w.routed_bytes, stream, !fused && need_extra ? w.extra : nullptr, KMOE_X_F16, &bl,
+                            qd_ride ? &qd : nullptr);
 }
 
 }  // extern "C"

@@ -121,9 +121,75 @@ struct Stage1Args {
   int wgs_per_token;        // workgroups working on each token
   uint16_t* sh_act;         // dense shared expert's SwiGLU output, 2 fp16 planes [T][Is] (or null)
   size_t sh_plane;          // T*Is
-  QLin ql;                  // router projection of extra workgroups (QL instantiations)
+  QLin ql;                  // router projection of extra workgroups (EX_QL instantiations)
   int ql_row_blocks;        // its workgroups: row blocks x token blocks
+  QDown qd;                 // one-expert down projection of extra workgroups (EX_QD instantiations)
 };
+
+// Down rows of a one-expert layer for workgroup b of the extra workgroups: LPR lanes per row (the
+// chunk count rounded up to a power of two), 64/LPR rows per wave, every token's act chunk (hi
+// and lo planes) dotted with the row's raw codes, s*2^24*dot + b*sum(act) per chunk, fp16 out
+// (the arithmetic of stage 2's per-assignment form).
+template <int BITS, bool BF16>
+__device__ __forceinline__ void qdown_rows(const QDown& Q, int H, int T, int b) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int I = Q.I, nch = I / CHUNK, ng = I / GROUP;
+  int lpr = 1;
+  while (lpr < nch && lpr < 64) lpr <<= 1;
+  const int rpw = 64 / lpr, cl = lane & (lpr - 1);
+  const int h = (b * 4 + wave) * rpw + lane / lpr;
+  const size_t rbytes = (size_t)I * BITS / 8;
+  float acc[DEC_MAX_TOKENS];
+#pragma unroll
+  for (int j = 0; j < DEC_MAX_TOKENS; ++j) acc[j] = 0.f;
+  if (h < H) {
+    for (int c = cl; c < nch; c += lpr) {
+      uint32_t d[4], cp[16];
+      load_chunk<BITS>(Q.d.w + (size_t)h * rbytes, c, d);
+      unpack_chunk<BITS, false>(d, cp);
+      const float sf = scale_to_f32<BF16>(Q.d.s[(size_t)h * ng + (c >> 1)]) * TWO24;
+      const float bf = scale_to_f32<BF16>(Q.d.b[(size_t)h * ng + (c >> 1)]);
+#pragma unroll
+      for (int j = 0; j < DEC_MAX_TOKENS; ++j) {
+        if (j < T) {
+          uint32_t xh[16], xl[16];
+          load16(Q.act + (size_t)j * I + (size_t)c * CHUNK, xh);
+          load16(Q.act + Q.plane + (size_t)j * I + (size_t)c * CHUNK, xl);
+          float sh = 0.f, sl = 0.f;
+#pragma unroll
+          for (int m = 0; m < 16; ++m) {
+            sh = fdot2(xh[m], ONE2, sh);
+            sl = fdot2(xl[m], ONE2, sl);
+          }
+          acc[j] += fmaf(sf, chunk_dot(cp, xh) + chunk_dot(cp, xl), bf * (sh + sl));
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < DEC_MAX_TOKENS; ++j) {
+    const float v = group_sum_last(acc[j], lpr);
+    if (cl == lpr - 1 && h < H && j < T) Q.y[(size_t)j * H + h] = f32_to_f16_bits(v);
+  }
+}
+
+__device__ __forceinline__ void dec_qdown_rows(const QDown& Q, int H, int T, int b) {
+  if (Q.bits == 3) {
+    if (Q.bf16) qdown_rows<3, true>(Q, H, T, b);
+    else qdown_rows<3, false>(Q, H, T, b);
+  } else {
+    if (Q.bf16) qdown_rows<4, true>(Q, H, T, b);
+    else qdown_rows<4, false>(Q, H, T, b);
+  }
+}
+
+// Extra workgroups of EX_QD: rows of H in blocks of 4 waves x 64/LPR rows.
+inline int qdown_workgroups(const QDown& Q, int H) {
+  int lpr = 1;
+  while (lpr < Q.I / CHUNK && lpr < 64) lpr <<= 1;
+  const int rows = 4 * (64 / lpr);
+  return (H + rows - 1) / rows;
+}
 
 // Rows of the dense fp16 shared expert per wave in the decode stages.
 constexpr int DEC_SH_RW = 2;
@@ -210,14 +276,24 @@ __device__ __forceinline__ void dec_shared_gateup(const uint16_t* __restrict__ x
 // The values the first loads need (logits, x, the sizes) come as leading scalar arguments: gfx950
 // preloads those into SGPRs at wave launch (the library is built with kernel-argument preload),
 // so the x and logits loads issue without waiting for the kernel-argument fetch.
-template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE, bool XS, bool SH, bool QL>
+// EX: the work of the workgroups past the routed ones: 0 none, EX_SH the dense shared expert's
+// gate/up rows, EX_QL the block's router projection, EX_QD the block's quantized shared expert's
+// down rows (its act from the shared layer's stage 1).
+constexpr int EX_SH = 1, EX_QL = 2, EX_QD = 3;
+template <int BITS, bool BF16, int ACT, int CPL, int RW, bool ROUTE, bool XS, int EX>
 __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict__ logits,
                                                          const void* __restrict__ x, int H, int E, int K, int I,
                                                          int wgs_per_token, int nrouted, const Stage1Args A) {
   const LayerArgs& L = A.L;
-  static_assert(!(SH && XS), "the dense shared expert takes fp16 activations only");
-  static_assert(!(QL && (XS || SH || ROUTE)), "the router projection rides along the block's shared layer only");
-  if constexpr (QL) {  // workgroups past the shared layer's: the block's router projection
+  static_assert(!(EX && XS), "the extra workgroups serve fp16 activations only");
+  static_assert(EX != EX_QL || !ROUTE, "the router projection rides along the block's shared layer only");
+  if constexpr (EX == EX_QD) {  // workgroups past the routed ones: the block's shared down rows
+    if ((int)blockIdx.x >= nrouted) {
+      dec_qdown_rows(A.qd, H, A.T, (int)blockIdx.x - nrouted);
+      return;
+    }
+  }
+  if constexpr (EX == EX_QL) {  // workgroups past the shared layer's: the block's router projection
     if ((int)blockIdx.x >= nrouted) {
       const int bid = (int)blockIdx.x - nrouted;
       qlinear_rows<BITS, BF16>(A.ql.a, A.ql.ra, A.ql.b, A.ql.rb, A.T, H, static_cast<const uint16_t*>(x), A.ql.out_a,
@@ -225,7 +301,7 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
       return;
     }
   }
-  if constexpr (SH) {  // workgroups past the routed ones: the dense shared expert's gate/up rows
+  if constexpr (EX == EX_SH) {  // workgroups past the routed ones: the dense shared expert's gate/up rows
     if ((int)blockIdx.x >= nrouted) {
       dec_shared_gateup<ACT>(static_cast<const uint16_t*>(x), A.T, H, L, A.sh_act, A.sh_plane,
                              (int)blockIdx.x - nrouted, (int)gridDim.x - nrouted);
@@ -901,8 +977,10 @@ template <typename KERN>
 static hipError_t launch_stage1(KERN k1, int grid, hipStream_t s, const Stage1Args& A) {
   // extra workgroups after the routed ones: the dense shared expert's gate/up rows (fp16
   // activations only) or the block's router projection
-  const int nsh = A.sh_act ? A.L.Is / (4 * DEC_SH_RW)
-                 : A.ql.out_a ? A.ql_row_blocks * qlinear_token_blocks(A.T) : 0;
+  const int nsh = A.sh_act     ? A.L.Is / (4 * DEC_SH_RW)
+                 : A.ql.out_a ? A.ql_row_blocks * qlinear_token_blocks(A.T)
+                 : A.qd.y     ? qdown_workgroups(A.qd, A.L.H)
+                              : 0;
   KMOE_LAUNCH("dec_stage1_kernel", k1, dim3(grid + nsh), dim3(256), 0, s, A.logits, A.x, A.L.H, A.L.E, A.K,
               A.L.I, A.wgs_per_token, grid, A);
   return hipGetLastError();
@@ -935,6 +1013,8 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   A.ql = d.ql ? *d.ql : QLin{};
   A.ql_row_blocks = qlinear_row_blocks(A.ql.ra + A.ql.rb);
   if (d.ql && (d.logits || d.xdt != XDT_F16)) return hipErrorInvalidValue;
+  A.qd = d.qd ? *d.qd : QDown{};
+  if (d.qd && (!d.logits || d.xdt != XDT_F16 || L.sh_gate || d.ql)) return hipErrorInvalidValue;
   A.wgs_per_expert = L.I / (4 * RW);
   // at most two workgroups per CU in all: every workgroup repeats its token's routing, so the
   // grid stays resident and loops over the token's (expert, row block) items instead
@@ -944,28 +1024,32 @@ static hipError_t decode_impl(const LayerConfig& c, const DecodeCall& d, hipStre
   auto stage1 = [&](auto xs) {
     constexpr bool XSV = decltype(xs)::value;
     if constexpr (!XSV) {
+      if (A.qd.y) {  // the block's shared down rows ride along (routing, fp16)
+        if (nch <= 64) return launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, false, EX_QD>, grid1, s, A);
+        return launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, false, EX_QD>, grid1, s, A);
+      }
       if (A.ql.out_a) {  // the block's router projection rides along (given indices, fp16)
         if (nch <= 64)
-          return launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, false, false, true>, grid1, s, A);
-        return launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, false, false, true>, grid1, s, A);
+          return launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, false, EX_QL>, grid1, s, A);
+        return launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, false, EX_QL>, grid1, s, A);
       }
       // the dense shared expert's gate/up rows ride along (fp16 activations)
       if (A.sh_act) {
         if (nch <= 64)
-          return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, false, true, false>, grid1, s, A)
-                          : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, false, true, false>, grid1, s, A);
-        return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, false, true, false>, grid1, s, A)
-                        : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, false, true, false>, grid1, s, A);
+          return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, false, EX_SH>, grid1, s, A)
+                          : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, false, EX_SH>, grid1, s, A);
+        return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, false, EX_SH>, grid1, s, A)
+                        : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, false, EX_SH>, grid1, s, A);
       }
     }
     if (nch <= 64)
-      return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, XSV, false, false>, grid1, s, A)
-                      : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, XSV, false, false>, grid1, s, A);
-    return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, XSV, false, false>, grid1, s, A)
-                    : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, XSV, false, false>, grid1, s, A);
+      return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, true, XSV, 0>, grid1, s, A)
+                      : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 1, RW, false, XSV, 0>, grid1, s, A);
+    return d.logits ? launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, true, XSV, 0>, grid1, s, A)
+                    : launch_stage1(&dec_stage1_kernel<BITS, BF16, ACT, 2, RW, false, XSV, 0>, grid1, s, A);
   };
   err = d.xdt == XDT_F16 ? stage1(std::false_type{}) : stage1(std::true_type{});
-  if (err != hipSuccess) return err;
+  if (err != hipSuccess || d.stage1_only) return err;
   const int l2 = lpa_log2_for(L.I);
   // Output rows per workgroup (S2_ROWS) and per lane (RPW), and tokens per workgroup (TG).  Every
   // workgroup re-reads the act rows of its tokens' assignments, so taller row blocks cut that

@@ -109,6 +109,17 @@ struct QLin {
   float* out_b = nullptr;
 };
 
+// The down projection of a one-expert layer (the MoE block's quantized shared expert) run by
+// extra workgroups of another layer's decode stage 1: y [T][H] fp16 from act (two fp16 planes
+// [T][I], the one-expert layer's stage-1 output in its pair order).
+struct QDown {
+  QProj d;
+  int bits = 0, bf16 = 0, I = 0;
+  const uint16_t* act = nullptr;
+  size_t plane = 0;
+  uint16_t* y = nullptr;
+};
+
 struct DecodeCall {
   const void* x;           // [T][H] of dtype xdt
   const float* logits;     // [T][E], or null when idx_in is given
@@ -126,6 +137,8 @@ struct DecodeCall {
   int xdt;                 // XDT_* of x
   Blend blend;             // block term added in the combine (decode only)
   const QLin* ql = nullptr; // router projection riding along stage 1 (given-indices mode only)
+  const QDown* qd = nullptr;  // one-expert down projection riding along stage 1 (routing mode)
+  bool stage1_only = false;   // launch stage 1 only (its act is consumed by a QDown elsewhere)
 };
 
 // Kernel timing hook (kmoe_profile_begin/end).  prof_events hands out the next event pair of
@@ -154,7 +167,8 @@ namespace kmoe {
 // those of kmoe_forward.
 int forward_impl(const kmoe_layer* layer, const void* x, const float* logits, int32_t tokens, void* out,
                  int32_t out_dtype, int32_t* idx_out, float* weights_out, void* workspace, size_t workspace_bytes,
-                 void* stream, const float* extra = nullptr, int xdt = XDT_F16, const Blend* blend = nullptr);
+                 void* stream, const float* extra = nullptr, int xdt = XDT_F16, const Blend* blend = nullptr,
+                 const QDown* qd = nullptr);
 // kmoe_workspace_size for `tokens` tokens of `layer`.
 int workspace_bytes_for(const kmoe_layer* layer, int32_t tokens, size_t* bytes);
 // Records `msg` as the calling thread's last error and returns `code`.
