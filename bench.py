@@ -11,8 +11,10 @@ captured sequence plus one captured partial sequence for the remainder).  Beside
 spread over at least 5 replays (at least 200 calls), decode at 4 and 8 tokens, the top-4 "fast
 mode", 4-bit decode (the 4-bit layer of the reference's CPU path), 3-bit prefill of
 512/2048/4096 Zipf-routed tokens, the hidden-2560 layer with its dense shared expert, the
-hidden-4096 / 512-expert / top-10 layer's 4096-token prefill, and one decode token through a
-stack of 60 such layers (169 GB resident).
+hidden-4096 / 512-expert / top-10 layer's 4096-token prefill, one decode token through a
+stack of 60 such layers (169 GB resident), the whole MoE block (router projection, routed
+experts, gated shared expert, residual) at 1 and 8 tokens, and the TQ3 expert MLP at 1 and 4
+tokens.
 
 `value` = achieved algorithmic HBM bandwidth of the layer at 1 token, in GB/s (with --decode
 lists that leave out 1:8, of the first case measured; `config` then names that case):
