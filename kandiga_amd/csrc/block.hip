@@ -21,11 +21,11 @@
 
 namespace kmoe {
 
-template <int BITS, bool BF16>
+template <int BITS, bool BF16, int RPW>
 __global__ __launch_bounds__(256) void qlinear_kernel(const QProj A, int ra, const QProj B, int rb, int T, int H,
                                                       const uint16_t* __restrict__ x, float* __restrict__ out_a,
                                                       float* __restrict__ out_b) {
-  qlinear_rows<BITS, BF16>(A, ra, B, rb, T, H, x, out_a, out_b, (int)blockIdx.x, (int)blockIdx.y);
+  qlinear_rows<BITS, BF16, RPW>(A, ra, B, rb, T, H, x, out_a, out_b, (int)blockIdx.x, (int)blockIdx.y);
 }
 
 __global__ __launch_bounds__(256) void blend_prep_kernel(const uint16_t* __restrict__ shared16,
@@ -70,9 +70,18 @@ hipError_t launch_qlinear(const QProj& a, int ra, const QProj& b, int rb, int bi
                           int T, int H, float* out_a, float* out_b, hipStream_t s) {
   const int R = ra + rb;
   if (T == 0 || R == 0) return hipSuccess;
-  const dim3 grid(qlinear_row_blocks(R), qlinear_token_blocks(T));
-#define KMOE_QL(BB, FF) \
-  KMOE_LAUNCH("qlinear_kernel", (qlinear_kernel<BB, FF>), grid, dim3(256), 0, s, a, ra, b, rb, T, H, x, out_a, out_b)
+  // eight rows per wave once the batch outgrows decode (the token blocks then fill the GPU)
+  const bool wide = T > DEC_MAX_TOKENS;
+  const dim3 grid(qlinear_row_blocks(R, wide ? 8 : QL_RPW), qlinear_token_blocks(T));
+#define KMOE_QL(BB, FF)                                                                                          \
+  do {                                                                                                           \
+    if (wide)                                                                                                    \
+      KMOE_LAUNCH("qlinear_kernel", (qlinear_kernel<BB, FF, 8>), grid, dim3(256), 0, s, a, ra, b, rb, T, H, x,      \
+                  out_a, out_b);                                                                                 \
+    else                                                                                                         \
+      KMOE_LAUNCH("qlinear_kernel", (qlinear_kernel<BB, FF, QL_RPW>), grid, dim3(256), 0, s, a, ra, b, rb, T, H, x, \
+                  out_a, out_b);                                                                                 \
+  } while (0)
   if (bits == 3) {
     if (bf16) KMOE_QL(3, true); else KMOE_QL(3, false);
   } else {
