@@ -358,7 +358,7 @@ int kmoe_expert_mlp_x(const kmoe_layer* layer, const void* x, int32_t x_dtype, c
     DecodeCall d{x, nullptr, idx, tokens, nullptr, nullptr, nullptr, &w, yy, 0, false, nullptr, x_dtype};
     e = launch_decode(c, d, s);
   } else {
-    const int bm = gemm_bm(c.args, x_dtype), mmt = max_mtiles_for(tokens * K, c.args.E, bm);
+    const int bm = gemm_bm(c.args, x_dtype, tokens * K), mmt = max_mtiles_for(tokens * K, c.args.E, bm);
     e = launch_permute(idx, tokens * K, K, c.args.E, w, mmt, bm, s);
     if (e == hipSuccess) e = launch_xpair(c, x, x_dtype, tokens, w.xpp, w.xinv, s);
     if (e == hipSuccess)
@@ -436,7 +436,7 @@ int kmoe::forward_impl(const kmoe_layer* layer, const void* x, const float* logi
     d.qd = qd;
     e = launch_decode(c, d, s);
   } else {
-    const int bm = gemm_bm(a, xdt), mmt = max_mtiles_for(tokens * K, a.E, bm);
+    const int bm = gemm_bm(a, xdt, tokens * K), mmt = max_mtiles_for(tokens * K, a.E, bm);
     e = launch_route_xpair(logits, tokens, a.E, K, w.idx, w.wts, x, xdt, a.H, c.bits, w.xpp, w.xinv, s);
     if (e == hipSuccess) e = launch_permute(w.idx, tokens * K, K, a.E, w, mmt, bm, s);
     if (e == hipSuccess)
@@ -773,7 +773,7 @@ int kmoe_block_forward(const kmoe_block* block, const void* x, const void* resid
       d.stage1_only = qd_ride;  // its down rows ride along the routed layer's stage 1
       e = launch_decode(sc, d, s);
     } else if (e == hipSuccess) {
-      const int bm = gemm_bm(sc.args), mmt = max_mtiles_for(tokens, 1, bm);
+      const int bm = gemm_bm(sc.args, XDT_F16, tokens), mmt = max_mtiles_for(tokens, 1, bm);
       e = launch_permute(w.idx0, tokens, 1, 1, w.sh, mmt, bm, s);
       if (e == hipSuccess) e = launch_xpair(sc, xx, KMOE_X_F16, tokens, w.sh.xpp, nullptr, s);
       if (e == hipSuccess) e = launch_gemm(sc, w.sh.xpp, tokens, w.sh, mmt, w.ysh, nullptr, s);

@@ -679,7 +679,7 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
   // weights from the prefill copy when the layer has one, else the MLX tensors with scales in
   // pairs of groups when the rows hold an even number of groups
   const bool pk = L.pk[0].codes != nullptr;
-  const int bm = gemm_bm(L, xdt);  // the m-tile list was built with this many rows per tile
+  const int bm = gemm_bm(L, xdt, T * c.top_k);  // the m-tile list was built with this many rows per tile
   const size_t xplane = (size_t)T * L.H;  // lo plane of fp32 activations
   const int bl_gu = pk ? 2 : (L.H / GROUP) % 2 == 0 ? 1 : 0;
   const int bl_dn = pk ? 2 : (L.I / GROUP) % 2 == 0 ? 1 : 0;
@@ -690,7 +690,9 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
     if (bl_gu == 2) KMOE_GU(2, 128, 2); else if (bl_gu == 1) KMOE_GU(1, 128, 2); else KMOE_GU(0, 128, 2);
   } else if (bl_gu == 2) {
     if (bm == 64) KMOE_GU(2, 64, 1); else KMOE_GU(2, 128, 1);
-  } else if (bl_gu == 1) KMOE_GU(1, 128, 1); else KMOE_GU(0, 128, 1);
+  } else if (bl_gu == 1) {
+    if (bm == 64) KMOE_GU(1, 64, 1); else KMOE_GU(1, 128, 1);
+  } else KMOE_GU(0, 128, 1);
 #undef KMOE_GU
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
@@ -702,11 +704,15 @@ static hipError_t gemm_impl(const LayerConfig& c, const uint16_t* x, int T, cons
   if (y16) {
     if (bl_dn == 2) {
       if (bm == 64) KMOE_DOWN(true, 2, 64); else KMOE_DOWN(true, 2, 128);
-    } else if (bl_dn == 1) KMOE_DOWN(true, 1, 128); else KMOE_DOWN(true, 0, 128);
+    } else if (bl_dn == 1) {
+      if (bm == 64) KMOE_DOWN(true, 1, 64); else KMOE_DOWN(true, 1, 128);
+    } else KMOE_DOWN(true, 0, 128);
   } else {
     if (bl_dn == 2) {
       if (bm == 64) KMOE_DOWN(false, 2, 64); else KMOE_DOWN(false, 2, 128);
-    } else if (bl_dn == 1) KMOE_DOWN(false, 1, 128); else KMOE_DOWN(false, 0, 128);
+    } else if (bl_dn == 1) {
+      if (bm == 64) KMOE_DOWN(false, 1, 64); else KMOE_DOWN(false, 1, 128);
+    } else KMOE_DOWN(false, 0, 128);
   }
 #undef KMOE_DOWN
   return hipGetLastError();
