@@ -186,15 +186,15 @@ hipError_t launch_permute(const int32_t* idx, int TK, int K, int E, const Work& 
                           hipStream_t s);
 // Tiles of 64 rows pay off with the prefill copy's cheap weight loads, up to a gate/up k loop of
 // 2048; past that the 128-row tile's weight reuse wins.  From the MLX layout they pay off for
-// batches of at most 4096 assignments (most experts then hold under 32 rows, and the two-plane
-// down GEMM runs half the padding; measured at 512 tokens, top-8) when both projections hold an
+// batches of at most 8192 assignments (most experts then hold under 64 rows, and the two-plane
+// down GEMM runs half the padding; measured at 512 and 1024 tokens, top-8) when both projections hold an
 // even number of groups per row.  fp32 activations (two A planes in the gate/up GEMM) always use
 // 128-row tiles.  tk = tokens * top_k of the call.
 inline int gemm_bm(const LayerArgs& a, int xdt = XDT_F16, int tk = 0) {
   if (xdt == XDT_F32 || a.H > 2048) return GEMM_BM;
   if (a.pk[0].codes) return GEMM_BM_PACK;
   const bool even = a.H % 128 == 0 && a.I % 128 == 0;  // two 64-wide groups per pair
-  return even && tk > 0 && tk <= 4096 ? GEMM_BM_PACK : GEMM_BM;
+  return even && tk > 0 && tk <= 8192 ? GEMM_BM_PACK : GEMM_BM;
 }
 hipError_t launch_decode(const LayerConfig& c, const DecodeCall& d, hipStream_t s);
 // x [T][H] -> xpp in pair order (per 32-wide chunk), the gate/up GEMM's A layout (bf16 / fp32
