@@ -348,19 +348,14 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
     }
   }
   int my = -1;
+  float myl = 0.f;  // routing wave: the selected logits (lane k < K)
   // one routing wave per workgroup: redundant copies in the other waves would share SIMDs with
-  // it and stretch its latency; they permute their x chunks and wait at the barrier instead
+  // it and stretch its latency; they permute their x chunks and wait at the barrier instead.
+  // Only the selection is on the path to the barrier; the weights come after it.
   __shared__ int32_t s_sel[16];
   if (ROUTE && wave == 0) {
-    float myw;
-    KMOE_TOPK_DISPATCH(E, (wave_topk_regs<EPL_>(logits + (size_t)t * E, E, K, my, myw)));
-    if (lane < K) {
-      s_sel[lane] = my;
-      if (lb == 0) {
-        if (A.idx_out) A.idx_out[t * K + lane] = my;
-        if (A.w_out) A.w_out[t * K + lane] = myw;
-      }
-    }
+    KMOE_TOPK_DISPATCH(E, (wave_topk_select_regs<EPL_>(logits + (size_t)t * E, E, K, my, myl)));
+    if (lane < K) s_sel[lane] = my;
   }
   KMOE_MARK(0, 1);
   // fp16 planes of the activations: as loaded (fp16), or scaled per token (bf16, fp32).  With
@@ -594,6 +589,15 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
   const int step = wgs_per_token;
   int item = lb;
   if (item < nitems) load_item(item, W0);
+  // the routing outputs: the routing wave of each token's first workgroup computes the weights
+  // while its first item's loads are in flight
+  if (ROUTE && lb == 0 && wave == 0) {
+    const float wv = topk_weight(myl, K);
+    if (lane < K) {
+      if (A.idx_out) A.idx_out[t * K + lane] = my;
+      if (A.w_out) A.w_out[t * K + lane] = wv;
+    }
+  }
   for (; item < nitems; item += 2 * step) {
     if (item + step < nitems) load_item(item + step, W1);
     compute_item(item, W0);

@@ -490,8 +490,11 @@ __device__ __forceinline__ void wave_load_logits(const float* __restrict__ row, 
   }
 }
 
+// The selection half of the top-K: lane k < K gets the k-th expert in `sel` and its logit in
+// `sel_l`; other lanes get -1 and 0.
 template <int EPL>
-__device__ __forceinline__ void wave_topk_vals(const float (&lv)[TOPK_MAX_EPL], int E, int K, int& sel, float& selw) {
+__device__ __forceinline__ void wave_topk_select(const float (&lv)[TOPK_MAX_EPL], int E, int K, int& sel,
+                                                 float& sel_l) {
   const int lane = threadIdx.x & 63;
   uint32_t kh[EPL], ke[EPL];  // key, ~index (larger ~index = lower index); padding: key 0, ~index 0
 #pragma unroll
@@ -500,12 +503,13 @@ __device__ __forceinline__ void wave_topk_vals(const float (&lv)[TOPK_MAX_EPL], 
     kh[m] = e < E ? logit_key(lv[m]) : 0u;
     ke[m] = e < E ? ~(uint32_t)e : 0u;
   }
-  // odd-even transposition sort, descending by (key, ~index)
+  // odd-even transposition sort, descending by key.  It swaps only on a strictly larger key,
+  // so equal keys keep their order, which is ascending index (padding, at the largest m, last).
 #pragma unroll
   for (int pass = 0; pass < EPL; ++pass) {
 #pragma unroll
     for (int j = pass & 1; j + 1 < EPL; j += 2) {
-      const bool sw = kh[j + 1] > kh[j] || (kh[j + 1] == kh[j] && ke[j + 1] > ke[j]);
+      const bool sw = kh[j + 1] > kh[j];
       const uint32_t h0 = kh[j], e0 = ke[j];
       kh[j] = sw ? kh[j + 1] : h0;
       ke[j] = sw ? ke[j + 1] : e0;
@@ -513,19 +517,23 @@ __device__ __forceinline__ void wave_topk_vals(const float (&lv)[TOPK_MAX_EPL], 
       ke[j + 1] = sw ? e0 : ke[j + 1];
     }
   }
-  int my = 0;
+  int my = -1;
   float my_l = 0.0f;
   for (int k = 0; k < K; ++k) {
     const uint32_t m = wave_max_u32_dpp(kh[0]);
-    const uint64_t holders = __ballot(kh[0] == m);
-    uint32_t einv;
+    const bool hold = kh[0] == m;
+    const uint64_t holders = __ballot(hold);
+    int e;
+    bool pop;
     if (__popcll(holders) == 1) {
-      einv = (uint32_t)__builtin_amdgcn_readlane((int)ke[0], (int)__builtin_ctzll(holders));
+      // the one holder pops; the index it held is only needed for the output
+      e = (int)~(uint32_t)__builtin_amdgcn_readlane((int)ke[0], (int)__builtin_ctzll(holders));
+      pop = hold;
     } else {
-      einv = wave_max_u32_dpp(kh[0] == m ? ke[0] : 0u);
+      e = (int)~wave_max_u32_dpp(hold ? ke[0] : 0u);
+      pop = lane == (e & 63);
     }
-    const int e = (int)~einv;
-    if (lane == (e & 63)) {  // pop the head
+    if (pop) {
 #pragma unroll
       for (int j = 0; j + 1 < EPL; ++j) {
         kh[j] = kh[j + 1];
@@ -539,13 +547,27 @@ __device__ __forceinline__ void wave_topk_vals(const float (&lv)[TOPK_MAX_EPL], 
       my_l = logit_from_key(m);
     }
   }
-  const float l0 = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(my_l)));
-  const float ex = lane < K ? expf(my_l - l0) : 0.0f;
+  sel = my;
+  sel_l = my_l;
+}
+
+// The weights half: lanes k < K hold the selected logits l_k (l_0 the largest); returns
+// exp(l_k - l_0) / sum_j exp(l_j - l_0), the sum taken in k order, in lane k and 0 elsewhere.
+__device__ __forceinline__ float topk_weight(float sel_l, int K) {
+  const int lane = threadIdx.x & 63;
+  const float l0 = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(sel_l)));
+  const float ex = lane < K ? expf(sel_l - l0) : 0.0f;
   float sum = 0.0f;
   for (int k = 0; k < K; ++k)
     sum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(ex), k));
-  sel = lane < K ? my : -1;
-  selw = lane < K ? ex / sum : 0.0f;
+  return lane < K ? ex / sum : 0.0f;
+}
+
+template <int EPL>
+__device__ __forceinline__ void wave_topk_vals(const float (&lv)[TOPK_MAX_EPL], int E, int K, int& sel, float& selw) {
+  float sel_l;
+  wave_topk_select<EPL>(lv, E, K, sel, sel_l);
+  selw = topk_weight(sel_l, K);
 }
 
 template <int EPL>
@@ -553,6 +575,14 @@ __device__ __forceinline__ void wave_topk_regs(const float* __restrict__ row, in
   float lv[TOPK_MAX_EPL];
   wave_load_logits(row, E, lv);
   wave_topk_vals<EPL>(lv, E, K, sel, selw);
+}
+
+template <int EPL>
+__device__ __forceinline__ void wave_topk_select_regs(const float* __restrict__ row, int E, int K, int& sel,
+                                                      float& sel_l) {
+  float lv[TOPK_MAX_EPL];
+  wave_load_logits(row, E, lv);
+  wave_topk_select<EPL>(lv, E, K, sel, sel_l);
 }
 
 // wave_topk_regs with the results stored: lanes k < K write idx_out[k] / w_out[k] (either may
