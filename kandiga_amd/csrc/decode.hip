@@ -600,9 +600,11 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
   }
   for (; item < nitems; item += 2 * step) {
     if (item + step < nitems) load_item(item + step, W1);
+    prio_by_work_left((nitems - item + step - 1) / step);
     compute_item(item, W0);
     if (item + step >= nitems) break;
     if (item + 2 * step < nitems) load_item(item + 2 * step, W0);
+    prio_by_work_left((nitems - item - 1) / step);
     compute_item(item + step, W1);
   }
   KMOE_MARK(0, 5);
@@ -772,12 +774,14 @@ __global__ __launch_bounds__(256) void dec_stage2_kernel(const int32_t* __restri
         U1 = unit_of(u + 4);
         load_unit(U1, S1);
       }
+      prio_by_work_left(nw - j);
       finish_unit(u, U0, S0);
       if (j + 1 >= nw) break;
       if (j + 2 < nw) {
         U0 = unit_of(u + 8);
         load_unit(U0, S0);
       }
+      prio_by_work_left(nw - j - 1);
       finish_unit(u + 4, U1, S1);
     }
   } else {

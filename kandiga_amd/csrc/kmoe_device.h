@@ -445,6 +445,21 @@ __device__ __forceinline__ void split_chunk(const float (&v)[32], float k, uint3
   }
 }
 
+// Issue priority of the calling wave by its work left (wave-uniform `left`, capped at 3).  Two
+// workgroups share each CU in the decode stages; by default the older one's waves win issue and
+// finish first, leaving the younger one to run its tail alone.  Waves with more work left take
+// precedence instead, so the two keep pace.
+__device__ __forceinline__ void prio_by_work_left(int left) {
+  if (left >= 3)
+    __builtin_amdgcn_s_setprio(3);
+  else if (left == 2)
+    __builtin_amdgcn_s_setprio(2);
+  else if (left == 1)
+    __builtin_amdgcn_s_setprio(1);
+  else
+    __builtin_amdgcn_s_setprio(0);
+}
+
 // Orderable key of a router logit: larger logit -> larger key, +0 == -0, NaN below all.
 __device__ __forceinline__ uint32_t logit_key(float v) {
   if (v != v) return 0u;
