@@ -352,10 +352,23 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
   // one routing wave per workgroup: redundant copies in the other waves would share SIMDs with
   // it and stretch its latency; they permute their x chunks and wait at the barrier instead.
   // Only the selection is on the path to the barrier; the weights come after it.
+  // With routing the token's K experts are distinct and in slot order, and its K * wpe items
+  // (slot item / wpe) are strided over its workgroups: a workgroup runs only the selection
+  // rounds up to the slot of its last item, so the workgroups of the early slots start their
+  // weight loads while the later slots are still being selected.  The workgroup holding the
+  // token's last item runs all K rounds and writes the routing outputs.
+  int kneed = K;
+  bool writer = lb == 0;
+  if constexpr (ROUTE) {
+    const int ni = K * A.wgs_per_expert;
+    const int last = lb < ni ? lb + (ni - 1 - lb) / wgs_per_token * wgs_per_token : -1;
+    kneed = last >= 0 ? last / A.wgs_per_expert + 1 : 0;
+    writer = lb == (ni - 1) % wgs_per_token;
+  }
   __shared__ int32_t s_sel[16];
   if (ROUTE && wave == 0) {
-    KMOE_TOPK_DISPATCH(E, (wave_topk_select_regs<EPL_>(logits + (size_t)t * E, E, K, my, myl)));
-    if (lane < K) s_sel[lane] = my;
+    KMOE_TOPK_DISPATCH(E, (wave_topk_select_regs<EPL_>(logits + (size_t)t * E, E, kneed, my, myl)));
+    if (lane < K) s_sel[lane] = my;  // -1 past the rounds run
   }
   KMOE_MARK(0, 1);
   // fp16 planes of the activations: as loaded (fp16), or scaled per token (bf16, fp32).  With
@@ -478,8 +491,8 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
     }
   }
   const uint64_t first_m = __ballot(first);
-  const int nu = __popcll(first_m);
-  if (lb == 0 && tid == 0 && __popcll(valid_m) != K) atomicOr(&A.scalars[2], DEVERR_BAD_EXPERT);
+  const int nu = ROUTE ? K : __popcll(first_m);
+  if (!ROUTE && lb == 0 && tid == 0 && __popcll(valid_m) != K) atomicOr(&A.scalars[2], DEVERR_BAD_EXPERT);
   KMOE_MARK(0, 3);
 
   constexpr int V = 2 * RW;  // reduced values per item: gate then up, of RW rows
@@ -496,8 +509,9 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
     cvo[q] = (uint32_t)c * Bits<BITS>::chunk_bytes;
     svo[q] = (uint32_t)(c >> 1) * 2u;
   }
-  // expert of the token's u-th distinct expert (uniform)
+  // expert of the token's u-th distinct expert (uniform); with routing, slot u
   auto item_expert = [&](int u) {
+    if constexpr (ROUTE) return __builtin_amdgcn_readlane(my, u);
     uint64_t fm = first_m;
     for (int q = 0; q < u; ++q) fm &= fm - 1ull;
     return __builtin_amdgcn_readlane(my, (int)__builtin_ctzll(fm));
@@ -589,9 +603,9 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
   const int step = wgs_per_token;
   int item = lb;
   if (item < nitems) load_item(item, W0);
-  // the routing outputs: the routing wave of each token's first workgroup computes the weights
-  // while its first item's loads are in flight
-  if (ROUTE && lb == 0 && wave == 0) {
+  // the routing outputs: the routing wave of the workgroup that ran all K rounds computes the
+  // weights while its first item's loads are in flight
+  if (ROUTE && writer && wave == 0) {
     const float wv = topk_weight(myl, K);
     if (lane < K) {
       if (A.idx_out) A.idx_out[t * K + lane] = my;
