@@ -360,10 +360,10 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
   int kneed = K;
   bool writer = lb == 0;
   if constexpr (ROUTE) {
-    const int ni = K * A.wgs_per_expert;
-    const int last = lb < ni ? lb + (ni - 1 - lb) / wgs_per_token * wgs_per_token : -1;
-    kneed = last >= 0 ? last / A.wgs_per_expert + 1 : 0;
-    writer = lb == (ni - 1) % wgs_per_token;
+    const int ni = K * A.wgs_per_expert, per = (ni + wgs_per_token - 1) / wgs_per_token;
+    const int last = min(ni, (lb + 1) * per) - 1;
+    kneed = last >= lb * per ? last / A.wgs_per_expert + 1 : 0;
+    writer = lb == (ni - 1) / per;
   }
   __shared__ int32_t s_sel[16];
   if (ROUTE && wave == 0) {
@@ -600,9 +600,11 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
     KMOE_MARK(0, 4);
   };
   WStage W0, W1;
-  const int step = wgs_per_token;
-  int item = lb;
-  if (item < nitems) load_item(item, W0);
+  // the workgroup's items: a contiguous range (consecutive row blocks, early slots first)
+  const int per = (nitems + wgs_per_token - 1) / wgs_per_token;
+  const int iend = min(nitems, (lb + 1) * per);
+  int item = lb * per;
+  if (item < iend) load_item(item, W0);
   // the routing outputs: the routing wave of the workgroup that ran all K rounds computes the
   // weights while its first item's loads are in flight
   if (ROUTE && writer && wave == 0) {
@@ -612,14 +614,14 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
       if (A.w_out) A.w_out[t * K + lane] = wv;
     }
   }
-  for (; item < nitems; item += 2 * step) {
-    if (item + step < nitems) load_item(item + step, W1);
-    prio_by_work_left((nitems - item + step - 1) / step);
+  for (; item < iend; item += 2) {
+    if (item + 1 < iend) load_item(item + 1, W1);
+    prio_by_work_left(iend - item);
     compute_item(item, W0);
-    if (item + step >= nitems) break;
-    if (item + 2 * step < nitems) load_item(item + 2 * step, W0);
-    prio_by_work_left((nitems - item - 1) / step);
-    compute_item(item + step, W1);
+    if (item + 1 >= iend) break;
+    if (item + 2 < iend) load_item(item + 2, W0);
+    prio_by_work_left(iend - item - 1);
+    compute_item(item + 1, W1);
   }
   KMOE_MARK(0, 5);
 }
