@@ -357,13 +357,16 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
   // rounds up to the slot of its last item, so the workgroups of the early slots start their
   // weight loads while the later slots are still being selected.  The workgroup holding the
   // token's last item runs all K rounds and writes the routing outputs.
+  // Items are taken in reverse workgroup order: the first-dispatched workgroups (older waves,
+  // which win issue on a shared CU) get the last slots, whose selection runs longest.
+  const int li = wgs_per_token - 1 - lb;
   int kneed = K;
   bool writer = lb == 0;
   if constexpr (ROUTE) {
     const int ni = K * A.wgs_per_expert, per = (ni + wgs_per_token - 1) / wgs_per_token;
-    const int last = min(ni, (lb + 1) * per) - 1;
-    kneed = last >= lb * per ? last / A.wgs_per_expert + 1 : 0;
-    writer = lb == (ni - 1) / per;
+    const int last = min(ni, (li + 1) * per) - 1;
+    kneed = last >= li * per ? last / A.wgs_per_expert + 1 : 0;
+    writer = li == (ni - 1) / per;
   }
   __shared__ int32_t s_sel[16];
   if (ROUTE && wave == 0) {
@@ -602,8 +605,8 @@ __global__ __launch_bounds__(256) void dec_stage1_kernel(const float* __restrict
   WStage W0, W1;
   // the workgroup's items: a contiguous range (consecutive row blocks, early slots first)
   const int per = (nitems + wgs_per_token - 1) / wgs_per_token;
-  const int iend = min(nitems, (lb + 1) * per);
-  int item = lb * per;
+  const int iend = min(nitems, (li + 1) * per);
+  int item = li * per;
   if (item < iend) load_item(item, W0);
   // the routing outputs: the routing wave of the workgroup that ran all K rounds computes the
   // weights while its first item's loads are in flight
